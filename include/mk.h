@@ -1,0 +1,171 @@
+/* libmk -- MI355X-native MiniCPM5 prefill / scoring path (gfx950), C ABI.
+ *
+ * The boundary replaces the reference plugin's device program
+ *     pallas.jax_op("minicpm5_mk::forward", mk_jax.mk_forward)      (plugin/minicpm5_mk/model.py:57-66)
+ * called as
+ *     op(ids, embed, cos, sin, final_norm, w_qkv, w_o, w_gu, w_down, s_qkv, s_o, s_gu, s_down,
+ *        a_qkv, a_o, a_gu, a_down, wl_qkv, wl_o, wl_gu, wl_down,
+ *        bs, seq, quant, n_q, n_kv, head_dim, eps, attn)           (model.py:749-751, order :40-41)
+ * plus its kernel-level pieces (super_gqa_v2, fused_qkv, fused_mlp, linear).
+ *
+ * Conventions
+ *   - Every pointer argument is a device pointer unless stated otherwise; no torch types cross the ABI.
+ *   - bf16 tensors are passed as raw 16-bit storage; layouts are row-major and named as in the reference.
+ *   - `stream` is a hipStream_t (NULL = the legacy default stream).  Calls are stream-ordered and
+ *     asynchronous unless stated otherwise; the library creates no host threads.
+ *   - The caller owns every buffer (weights, packed weights, workspace, inputs, outputs).  The
+ *     library owns only the mk_model metadata, its cached hipGraphExec objects and one capture stream.
+ *   - Return value: MK_OK (0) or a negative MK_E* code; mk_last_error() gives a thread-local message.
+ */
+#ifndef MK_H_
+#define MK_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MK_OK 0
+#define MK_EINVAL -1       /* bad shape / argument / quant string           */
+#define MK_EHIP -2         /* a HIP runtime call failed                       */
+#define MK_EUNSUPPORTED -3 /* valid for the reference, not built here (fp8)   */
+#define MK_ENOMEM -4       /* caller-provided buffer too small                */
+
+/* Model dimensions: the reference's _mk_cfg (model.py:561-567) plus vocab and RoPE table rows. */
+typedef struct mk_config {
+  int32_t num_layers; /* L: L-1 full-sequence layers + 1 last-token-only layer (mk_jax.py:527-569) */
+  int32_t hidden;     /* H */
+  int32_t inter;      /* I */
+  int32_t n_q;        /* query heads (16) */
+  int32_t n_kv;       /* kv heads (2); n_q must be 8 * n_kv */
+  int32_t head_dim;   /* 64, 96 or 128 */
+  int32_t vocab;      /* V: rows of embed / lm_head */
+  float eps;          /* rms_norm_eps */
+  int32_t max_seq;    /* rows of the cos / sin tables */
+} mk_config;
+
+/* Device tensors in the reference's layout (prepare_mk_weights, mk_weights.py:126-263):
+ *   embed (V, H) bf16; cos, sin (max_seq, hd) bf16; final_norm (H) bf16;
+ *   w_qkv (L-1, H, (n_q + 2 n_kv) hd)   int8 or bf16, q columns pre-scaled by 1/sqrt(hd);
+ *   w_o   (L-1, n_q hd, H)              int8 or bf16;
+ *   w_gu  (L-1, H, 2I) chunk-interleaved [g_c | u_c] (flag fmlp) or (L-1, H, 2, I), int8 or bf16;
+ *   w_down(L-1, I, H)                   int8 or bf16;
+ *   s_* (L-1, out) f32 per-output-channel scales (s_gu (L-1, 1, 2I) in w_gu's column order);
+ *   a_* (L-1, in) f32 per-input-channel activation factors;  bf16 linears pass (L-1, 1) dummies;
+ *   wl_qkv (H, D), wl_o (q_dim, H), wl_gu (H, 2, I), wl_down (I, H) bf16 (last layer, gamma folded);
+ *   lm_head (V, H) bf16 (HF layout), optional: NULL means no logits. */
+typedef struct mk_weights {
+  const void* embed;
+  const void* cos;
+  const void* sin;
+  const void* final_norm;
+  const void* w_qkv;
+  const void* w_o;
+  const void* w_gu;
+  const void* w_down;
+  const float* s_qkv;
+  const float* s_o;
+  const float* s_gu;
+  const float* s_down;
+  const float* a_qkv;
+  const float* a_o;
+  const float* a_gu;
+  const float* a_down;
+  const void* wl_qkv;
+  const void* wl_o;
+  const void* wl_gu;
+  const void* wl_down;
+  const void* lm_head;
+} mk_weights;
+
+typedef struct mk_model mk_model;
+
+/* Thread-local message of the last failing call (never NULL). */
+const char* mk_last_error(void);
+/* ABI version (bumped on any signature change). */
+int mk_abi_version(void);
+
+/* Host-only validation of a config / quant string / (bs, seq) without touching the GPU.
+ * Mirrors the reference's trace-time asserts (mk_attn.py:672-673, mk_mlp.py:119,185) and the fast-path
+ * length rule _mk_seq_ok (model.py:131-136) restricted to what the kernels support (seq % 256 == 0). */
+int mk_validate(const mk_config* cfg, const char* quant, int bs, int seq);
+
+/* Bytes of the packed-weight buffer mk_model_create needs (host-only). */
+int mk_packed_bytes(const mk_config* cfg, const char* quant, size_t* bytes);
+
+/* Build a model: repacks the reference-layout weights into `packed` (K-contiguous MFMA layout)
+ * on `stream` and synchronizes it.  Replaces the op construction + weight upload of _mk_build
+ * (model.py:623-698).  The weight pointers must stay valid for the model's lifetime. */
+int mk_model_create(const mk_config* cfg, const char* quant, const mk_weights* w, void* packed,
+                    size_t packed_bytes, void* stream, mk_model** out);
+int mk_model_destroy(mk_model* m);
+
+/* Workspace bytes of one forward at (bs, seq) (host-only). */
+int mk_workspace_bytes(const mk_model* m, int bs, int seq, size_t* bytes);
+
+/* Whole-model prefill (mk_forward, mk_jax.py:624-665): ids (bs * seq) int32 sequence-major ->
+ * hidden_out (max(8, bs), H) bf16, row b = final-normed last-token hidden of sequence b, rows >= bs
+ * zero (pad_reqs, mk_jax.py:608-612).  logits_out (bs, V) f32 = hidden @ lm_head^T when non-NULL
+ * (the inherited vLLM LM head, model.py:224-235).  The launch sequence is captured once per
+ * (bs, seq, buffers) into a hipGraph and replayed. */
+int mk_forward(mk_model* m, const int32_t* input_ids, int bs, int seq, void* hidden_out, float* logits_out,
+               void* workspace, size_t workspace_bytes, void* stream);
+
+/* 1 (default) replays captured hipGraphs, 0 launches kernels eagerly on every call. */
+int mk_set_graph_mode(mk_model* m, int enable);
+
+/* ---------------------------------------------------------------- kernel-level entry points */
+
+/* Causal GQA prefill attention (super_gqa_v2, mk_attn.py:660-710): qkv (B, S, (n_q + 2 n_kv) hd) bf16
+ * -> out (B, S, n_q hd) bf16, RoPE from the bf16 cos / sin tables applied in-kernel, softmax in f32
+ * with scores scaled by sm_scale (pass 1.0 when 1/sqrt(hd) is folded into W_q, as the plugin does).
+ * scratch: mk_attn_scratch_bytes(B, S, n_kv, hd) bytes. */
+size_t mk_attn_scratch_bytes(int B, int S, int n_kv, int head_dim);
+int mk_attn_prefill(const void* qkv, const void* cos, const void* sin, void* out, void* scratch,
+                    size_t scratch_bytes, int B, int S, int n_q, int n_kv, int head_dim, float sm_scale,
+                    void* stream);
+
+/* Per-token dynamic int8 quantisation of rows x (T, H) (bf16, or f32 when x_f32):
+ *   norm:  rstd = rsqrt(mean(x^2) + eps), else 1;  u = x * a (a NULL = ones);
+ *   s = max(amax|u| / 127, 1e-6);  q = round_half_even(u * (1/s)) (fused: recip = 1) or u / s;
+ *   sx = s * rstd.
+ * The prologue of fused_qkv / fused_mlp (mk_mlp.py:161-168, recip 1, norm 1) and of the int8d
+ * linear / linear_rmsnorm (mk_jax.py:257-262,283-286, recip 0). */
+int mk_row_quant(const void* x, int x_f32, const float* a, int T, int H, float eps, int norm, int recip,
+                 int8_t* q, float* sx, void* stream);
+
+/* Epilogues of mk_gemm (C = A(M, K) B(N, K)^T, A and B K-contiguous):                       */
+#define MK_EPI_DQ_BF16 0        /* out bf16 = bf16((acc * rs[m]) * cs[n])        fused_qkv     */
+#define MK_EPI_DQ_SILU 1        /* out bf16 (M, N/2) = silu(g) * u, 32-col g/u interleave       */
+#define MK_EPI_DQ_SILU_F32A 2   /* out f32 (M, N/2) = silu(g) * u * aux[n']      int8 down in   */
+#define MK_EPI_BF16 3           /* out bf16 = bf16(acc)                                         */
+#define MK_EPI_F32 4            /* out f32 = acc                                                */
+#define MK_EPI_RES_BF16ADD 5    /* res = bf16(res + bf16(acc))                    bf16 O proj   */
+#define MK_EPI_DQ_RES_BF16ADD 6 /* res = bf16(res + bf16((acc * rs[m]) * cs[n])) int8d O proj  */
+#define MK_EPI_RES_F32ADD 7     /* res = bf16(res + acc)                          fused down    */
+#define MK_EPI_DQ2_RES_F32ADD 8 /* res = bf16(res + acc * (rs[m] * cs[n]))       int8 down     */
+#define MK_EPI_I32 9            /* out int32 = acc (int8 operands only)                         */
+#define MK_EPI_SILU_BF16 10     /* out bf16 (M, N/2): g,u = bf16(acc [* (rs[m] * cs[n])]), h = bf16(bf16(silu(g)) * u) */
+#define MK_EPI_DQ2_BF16 11      /* out bf16 = bf16(acc * (rs[m] * cs[n]))         linear_rmsnorm int8d */
+
+/* int8 x int8 -> int32 (is_int8 = 1) or bf16 x bf16 -> f32 MFMA GEMM with a fused epilogue. */
+int mk_gemm(int is_int8, int epi, const void* A, int lda, const void* B, int ldb, int M, int N, int K,
+            void* out, int ldo, void* res, int ldr, const float* rs, const float* cs, const float* aux,
+            void* stream);
+
+/* Last-token LM head: logits (B, V) f32 = hidden (B, H) bf16 @ lm_head (V, H)^T, any B. */
+int mk_lm_head(const void* hidden, const void* lm_head, int B, int H, int V, float* logits, void* stream);
+
+/* Weight repack (used by mk_model_create; exported for tests): out (N, K) = in (K, N)^T.
+ * map 1: N == 2 * inter columns in the reference's gate/up layout with chunk ic, reordered into
+ * 32-column gate/up interleave blocks. */
+int mk_pack_weight(const void* in, int ld_in, void* out, int K, int N, int elem_bytes, int map, int ic,
+                   int inter, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MK_H_ */

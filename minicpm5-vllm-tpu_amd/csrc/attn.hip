@@ -1,0 +1,435 @@
+// Causal GQA prefill attention for MiniCPM5 (gfx950).
+//
+// Reference: plugin/minicpm5_mk/mk_attn.py:557-710 (`super_gqa_v2`): causal GQA flash attention
+// with RoPE applied on load, log2(e) folded into Q, online softmax in f32, bf16 P for the PV
+// product, row-sum accumulated from that bf16 P, and a reciprocal epilogue.
+//
+// MI355X design:
+//   * attn_prep_kernel: K is RoPE'd once per sequence and written (B, n_kv, S, hd); V is written
+//     transposed (B, n_kv, hd, S) so that the PV contraction (over keys) is contiguous per lane.
+//     The reference builds the RoPE'd K and V' once per sequence too (mk_attn.py:568-580).
+//   * attn_fwd_kernel: one workgroup = (sequence, kv head, two 32-token q tiles paired
+//     zig-zag so every workgroup does the same causal work).  Its 8 waves are the 8 q heads of the
+//     kv head (GQA stacking, mk_attn.py:584-589); they share every K / V^T tile staged in LDS
+//     (double-buffered, prefetched through registers).  Each wave computes S^T = K Q^T with
+//     v_mfma_f32_32x32x16_bf16, so a lane owns one query's scores (column of the tile) and the
+//     row max / row sum need only in-lane work plus one exchange between the two lane halves.
+//     The accumulator layout of S^T is exactly the B-operand layout P^T needs for O^T = V^T P^T,
+//     so P never leaves registers.
+#include "kernels.h"
+#include "mk_common.h"
+
+namespace mk {
+
+namespace {
+
+constexpr int QT = 32;   // tokens per q tile (MFMA column block)
+constexpr int KT = 64;   // keys per K/V tile
+constexpr int G = 8;     // q heads per kv head == waves per workgroup
+constexpr int NT = 64 * G;
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_prep_kernel(const uint16_t* __restrict__ qkv,
+                                                        const uint16_t* __restrict__ cosr,
+                                                        const uint16_t* __restrict__ sinr,
+                                                        uint16_t* __restrict__ krope,
+                                                        uint16_t* __restrict__ vt, int S, int n_q,
+                                                        int n_kv) {
+  __shared__ uint16_t vs[64][HD + 2];
+  const int t0 = blockIdx.x * 64, kv = blockIdx.y, b = blockIdx.z;
+  const int D = (n_q + 2 * n_kv) * HD;
+  const uint16_t* base = qkv + ((size_t)b * S + t0) * D;
+  constexpr int H2 = HD / 2;
+  uint16_t* kdst = krope + (((size_t)b * n_kv + kv) * S + t0) * HD;
+  for (int idx = threadIdx.x; idx < 64 * H2; idx += 256) {
+    const int t = idx / H2, d = idx % H2;
+    const uint16_t* kr = base + (size_t)t * D + (n_q + kv) * HD;
+    const float x1 = bf2f(kr[d]), x2 = bf2f(kr[d + H2]);
+    const size_t tb = (size_t)(t0 + t) * HD;
+    const float c1 = bf2f(cosr[tb + d]), s1 = bf2f(sinr[tb + d]);
+    const float c2 = bf2f(cosr[tb + d + H2]), s2 = bf2f(sinr[tb + d + H2]);
+    kdst[(size_t)t * HD + d] = f2bf(x1 * c1 - x2 * s1);
+    kdst[(size_t)t * HD + d + H2] = f2bf(x2 * c2 + x1 * s2);
+  }
+  for (int idx = threadIdx.x; idx < 64 * HD; idx += 256) {
+    const int t = idx / HD, d = idx % HD;
+    vs[t][d] = base[(size_t)t * D + (n_q + n_kv + kv) * HD + d];
+  }
+  __syncthreads();
+  uint16_t* vdst = vt + ((size_t)b * n_kv + kv) * HD * S + t0;
+  for (int idx = threadIdx.x; idx < 64 * HD; idx += 256) {
+    const int d = idx / 64, t = idx % 64;
+    vdst[(size_t)d * S + t] = vs[t][d];
+  }
+}
+
+template <int HD>
+struct AttnSmem {
+  static constexpr int KROW = HD * 2 + 16;   // bytes per K row (padded)
+  static constexpr int VROW = KT * 2 + 16;   // bytes per V^T row (padded)
+  static constexpr int KBYTES = KT * KROW;
+  static constexpr int VBYTES = HD * VROW;
+  static constexpr int STAGE = KBYTES + VBYTES;
+  static constexpr int TOTAL = 2 * STAGE;
+  static constexpr int KCH = KT * HD / 8;      // 16-byte chunks per K tile
+  static constexpr int VCH = HD * KT / 8;      // 16-byte chunks per V^T tile
+  static constexpr int KPT = (KCH + NT - 1) / NT;
+  static constexpr int VPT = (VCH + NT - 1) / NT;
+};
+
+template <int HD>
+__global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
+    const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ cosr,
+    const uint16_t* __restrict__ sinr, const uint16_t* __restrict__ krope,
+    const uint16_t* __restrict__ vt, uint16_t* __restrict__ out, int S, int n_q, int n_kv,
+    float qscale) {
+  using L = AttnSmem<HD>;
+  constexpr int KS = HD / 16;   // k-steps of QK^T
+  constexpr int DT = HD / 32;   // 32-row d tiles of O^T
+  __shared__ __attribute__((aligned(16))) char smem[L::TOTAL];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, w = tid >> 6;
+  const int col = lane & 31, half = lane >> 5;
+  const int kv = blockIdx.y, b = blockIdx.z;
+  const int ntiles = S / QT;
+  const int D = (n_q + 2 * n_kv) * HD;
+  const int head = kv * G + w;
+  const uint16_t* kg = krope + ((size_t)b * n_kv + kv) * (size_t)S * HD;
+  const uint16_t* vg = vt + ((size_t)b * n_kv + kv) * (size_t)HD * S;
+
+  for (int pass = 0; pass < 2; ++pass) {
+    const int qt = pass == 0 ? (int)blockIdx.x : ntiles - 1 - (int)blockIdx.x;
+    const int t0 = qt * QT;
+    const int tok = t0 + col;
+
+    // ---- Q^T operand: RoPE in f32 from bf16 q and bf16 tables, scaled, rounded once to bf16.
+    u32x4 qreg[KS];
+    {
+      const uint16_t* qrow = qkv + ((size_t)b * S + tok) * D + head * HD;
+      const uint16_t* crow = cosr + (size_t)tok * HD;
+      const uint16_t* srow = sinr + (size_t)tok * HD;
+      u32x4 raw[KS];
+#pragma unroll
+      for (int s = 0; s < KS; ++s) raw[s] = *reinterpret_cast<const u32x4*>(qrow + 16 * s + 8 * half);
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const int ps = s < KS / 2 ? s + KS / 2 : s - KS / 2;
+        const float sg = s < KS / 2 ? -1.f : 1.f;
+        const u32x4 cv = *reinterpret_cast<const u32x4*>(crow + 16 * s + 8 * half);
+        const u32x4 sv = *reinterpret_cast<const u32x4*>(srow + 16 * s + 8 * half);
+        u32x4 r;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float x0 = bf_lo(raw[s][e]), x1 = bf_hi(raw[s][e]);
+          const float y0 = bf_lo(raw[ps][e]), y1 = bf_hi(raw[ps][e]);
+          const float r0 = (x0 * bf_lo(cv[e]) + sg * y0 * bf_lo(sv[e])) * qscale;
+          const float r1 = (x1 * bf_hi(cv[e]) + sg * y1 * bf_hi(sv[e])) * qscale;
+          r[e] = pack_bf2(r0, r1);
+        }
+        qreg[s] = r;
+      }
+    }
+
+    const int nkt = (t0 + QT - 1) / KT + 1;
+    f32x16 o[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) o[dt] = f32x16{};
+    float m = -INFINITY, l = 0.f;
+
+    u32x4 kst[L::KPT], vst[L::VPT];
+    auto gload = [&](int kt) {
+#pragma unroll
+      for (int i = 0; i < L::KPT; ++i) {
+        const int c = tid + i * NT;
+        if (c < L::KCH) {
+          const int key = c / (HD / 8), dc = c % (HD / 8);
+          kst[i] = *reinterpret_cast<const u32x4*>(kg + (size_t)(kt * KT + key) * HD + dc * 8);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < L::VPT; ++i) {
+        const int c = tid + i * NT;
+        if (c < L::VCH) {
+          const int d = c / (KT / 8), kc = c % (KT / 8);
+          vst[i] = *reinterpret_cast<const u32x4*>(vg + (size_t)d * S + kt * KT + kc * 8);
+        }
+      }
+    };
+    auto sstore = [&](int buf) {
+      char* ks = smem + buf * L::STAGE;
+      char* vs = ks + L::KBYTES;
+#pragma unroll
+      for (int i = 0; i < L::KPT; ++i) {
+        const int c = tid + i * NT;
+        if (c < L::KCH) {
+          const int key = c / (HD / 8), dc = c % (HD / 8);
+          *reinterpret_cast<u32x4*>(ks + key * L::KROW + dc * 16) = kst[i];
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < L::VPT; ++i) {
+        const int c = tid + i * NT;
+        if (c < L::VCH) {
+          const int d = c / (KT / 8), kc = c % (KT / 8);
+          *reinterpret_cast<u32x4*>(vs + d * L::VROW + kc * 16) = vst[i];
+        }
+      }
+    };
+
+    __syncthreads();  // previous pass finished reading the LDS stages
+    gload(0);
+    sstore(0);
+    __syncthreads();
+
+    for (int kt = 0; kt < nkt; ++kt) {
+      if (kt + 1 < nkt) gload(kt + 1);
+      const char* ks = smem + (kt & 1) * L::STAGE;
+      const char* vs = ks + L::KBYTES;
+
+      // S^T (64 keys x 32 tokens) = K Q^T
+      f32x16 sacc[2] = {f32x16{}, f32x16{}};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const u32x4 a0 = *reinterpret_cast<const u32x4*>(ks + col * L::KROW + (16 * s + 8 * half) * 2);
+        const u32x4 a1 =
+            *reinterpret_cast<const u32x4*>(ks + (32 + col) * L::KROW + (16 * s + 8 * half) * 2);
+        sacc[0] = mfma_bf16_32x32x16(a0, qreg[s], sacc[0]);
+        sacc[1] = mfma_bf16_32x32x16(a1, qreg[s], sacc[1]);
+      }
+      const int k0 = kt * KT;
+      if (k0 + KT - 1 > t0) {  // tile crosses the diagonal: mask keys after the query
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = k0 + 32 * c + 8 * (r >> 2) + 4 * half + (r & 3);
+            if (key > tok) sacc[c][r] = -INFINITY;
+          }
+      }
+      float mx = sacc[0][0];
+#pragma unroll
+      for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sacc[0][r]);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[1][r]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float mnew = fmaxf(m, mx);
+      const float alpha = fast_exp2(m - mnew);
+      m = mnew;
+
+      u32x4 pb[2][2];
+      float psum = 0.f;
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          u32x4 v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float p0 = fast_exp2(sacc[c][8 * s2 + 2 * e] - mnew);
+            const float p1 = fast_exp2(sacc[c][8 * s2 + 2 * e + 1] - mnew);
+            const uint32_t pk = pack_bf2(p0, p1);
+            psum += bf_lo(pk) + bf_hi(pk);
+            v[e] = pk;
+          }
+          pb[c][s2] = v;
+        }
+      l = l * alpha + psum;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+
+      // O^T (hd x 32 tokens) += V^T P^T
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const int key0 = 32 * c + 16 * s2 + 4 * half;
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) {
+            const char* vrow = vs + (dt * 32 + col) * L::VROW;
+            const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow + key0 * 2);
+            const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + (key0 + 8) * 2);
+            const u32x4 a = {lo[0], lo[1], hi[0], hi[1]};
+            o[dt] = mfma_bf16_32x32x16(a, pb[c][s2], o[dt]);
+          }
+        }
+
+      if (kt + 1 < nkt) sstore((kt + 1) & 1);
+      __syncthreads();
+    }
+
+    l += __shfl_xor(l, 32, 64);
+    const float inv = 1.f / l;
+    uint16_t* orow = out + ((size_t)b * S + tok) * (size_t)(n_q * HD) + head * HD;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int d0 = dt * 32 + 8 * i + 4 * half;
+        u32x2 v = {pack_bf2(o[dt][4 * i] * inv, o[dt][4 * i + 1] * inv),
+                   pack_bf2(o[dt][4 * i + 2] * inv, o[dt][4 * i + 3] * inv)};
+        *reinterpret_cast<u32x2*>(orow + d0) = v;
+      }
+  }
+}
+
+template <int HD>
+int launch_attn_hd(const AttnArgs& a, hipStream_t st) {
+  const dim3 pg(a.S / 64, a.n_kv, a.B);
+  hipLaunchKernelGGL(attn_prep_kernel<HD>, pg, dim3(256), 0, st, a.qkv, a.cos, a.sin, a.krope, a.vt,
+                     a.S, a.n_q, a.n_kv);
+  MK_HIP_CHECK(hipGetLastError());
+  const dim3 fg(a.S / QT / 2, a.n_kv, a.B);
+  hipLaunchKernelGGL(attn_fwd_kernel<HD>, fg, dim3(NT), 0, st, a.qkv, a.cos, a.sin, a.krope, a.vt,
+                     a.out, a.S, a.n_q, a.n_kv, a.qscale);
+  MK_HIP_CHECK(hipGetLastError());
+  return MK_OK;
+}
+
+
+// ---- last-token attention (mk_jax.py:492-520): one query per sequence against all S keys.
+// Kernel 1: workgroup = (256-key chunk, kv head, sequence); thread = key.  Writes per (head,
+// chunk) the partial max m, sum l = sum exp(s - m) and o = sum exp(s - m) v.  Kernel 2 merges the
+// chunks.  RoPE (position S-1 for q, the key's position for k) is computed in f32 and rounded to
+// bf16, as apply_rope_4d returns bf16 (mk_jax.py:48-52); scores and softmax are f32.
+constexpr int LCH = 256;
+
+template <int HD>
+__global__ __launch_bounds__(LCH) void last_attn_part_kernel(LastAttnArgs a) {
+  __shared__ float qs[G][HD];
+  __shared__ float ps[G][LCH];
+  __shared__ float red[G][LCH / 64];
+  const int chunk = blockIdx.x, kv = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
+  const int nchunk = a.S / LCH;
+  constexpr int H2 = HD / 2;
+  const size_t pos_last = (size_t)(a.S - 1) * HD;
+  for (int i = tid; i < G * HD; i += LCH) {
+    const int h = i / HD, d = i % HD;
+    const uint16_t* q = a.q + ((size_t)b * a.n_q + kv * G + h) * HD;
+    const float x = bf2f(q[d]);
+    const float y = d < H2 ? -bf2f(q[d + H2]) : bf2f(q[d - H2]);
+    qs[h][d] = bf2f(f2bf(x * bf2f(a.cos[pos_last + d]) + y * bf2f(a.sin[pos_last + d])));
+  }
+  __syncthreads();
+  const int t = chunk * LCH + tid;
+  const int kvdim = a.n_kv * HD;
+  const uint16_t* krow = a.kv + ((size_t)b * a.S + t) * (2 * kvdim) + kv * HD;
+  float s[G];
+#pragma unroll
+  for (int h = 0; h < G; ++h) s[h] = 0.f;
+  for (int d = 0; d < H2; ++d) {
+    const float x1 = bf2f(krow[d]), x2 = bf2f(krow[d + H2]);
+    const size_t tb = (size_t)t * HD;
+    const float k1 = bf2f(f2bf(x1 * bf2f(a.cos[tb + d]) - x2 * bf2f(a.sin[tb + d])));
+    const float k2 = bf2f(f2bf(x2 * bf2f(a.cos[tb + d + H2]) + x1 * bf2f(a.sin[tb + d + H2])));
+#pragma unroll
+    for (int h = 0; h < G; ++h) s[h] += qs[h][d] * k1 + qs[h][d + H2] * k2;
+  }
+  // block max per head
+  const int lane = tid & 63, w = tid >> 6;
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    float v = s[h];
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    if (lane == 0) red[h][w] = v;
+  }
+  __syncthreads();
+  float mh[G];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    float v = red[h][0];
+    for (int i = 1; i < LCH / 64; ++i) v = fmaxf(v, red[h][i]);
+    mh[h] = v;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    const float p = __expf(s[h] - mh[h]);
+    ps[h][tid] = p;
+    float v = p;
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    if (lane == 0) red[h][w] = v;
+  }
+  __syncthreads();
+  const uint16_t* vbase = a.kv + ((size_t)b * a.S + chunk * LCH) * (2 * kvdim) + kvdim + kv * HD;
+  for (int i = tid; i < G * HD; i += LCH) {
+    const int h = i / HD, d = i % HD;
+    float o = 0.f;
+    for (int k = 0; k < LCH; ++k) o += ps[h][k] * bf2f(vbase[(size_t)k * 2 * kvdim + d]);
+    float* pp = a.part + (((size_t)b * a.n_q + kv * G + h) * nchunk + chunk) * (HD + 2);
+    pp[2 + d] = o;
+    if (d == 0) {
+      float l = 0.f;
+      for (int j = 0; j < LCH / 64; ++j) l += red[h][j];
+      pp[0] = mh[h];
+      pp[1] = l;
+    }
+  }
+}
+
+template <int HD>
+__global__ void last_attn_merge_kernel(LastAttnArgs a) {
+  const int head = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+  const int nchunk = a.S / LCH;
+  const float* pp = a.part + ((size_t)b * a.n_q + head) * nchunk * (HD + 2);
+  float M = -INFINITY;
+  for (int c = 0; c < nchunk; ++c) M = fmaxf(M, pp[(size_t)c * (HD + 2)]);
+  float l = 0.f, o = 0.f;
+  for (int c = 0; c < nchunk; ++c) {
+    const float e = __expf(pp[(size_t)c * (HD + 2)] - M);
+    l += pp[(size_t)c * (HD + 2) + 1] * e;
+    o += pp[(size_t)c * (HD + 2) + 2 + d] * e;
+  }
+  a.out[((size_t)b * a.n_q + head) * HD + d] = f2bf(o / l);
+}
+
+template <int HD>
+int launch_last_attn_hd(const LastAttnArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL(last_attn_part_kernel<HD>, dim3(a.S / LCH, a.n_kv, a.B), dim3(LCH), 0, st, a);
+  MK_HIP_CHECK(hipGetLastError());
+  hipLaunchKernelGGL(last_attn_merge_kernel<HD>, dim3(a.n_q, a.B), dim3(HD), 0, st, a);
+  MK_HIP_CHECK(hipGetLastError());
+  return MK_OK;
+}
+
+}  // namespace
+
+int attn_validate(int B, int S, int n_q, int n_kv, int hd) {
+  MK_REQUIRE(B >= 1, "attention: batch must be >= 1");
+  MK_REQUIRE(S >= 64 && S % 64 == 0, "attention: seq must be a positive multiple of 64");
+  MK_REQUIRE(n_kv >= 1 && n_q == G * n_kv, "attention: n_q must equal 8 * n_kv (GQA group of 8)");
+  MK_REQUIRE(hd == 64 || hd == 96 || hd == 128, "attention: head_dim must be 64, 96 or 128");
+  return MK_OK;
+}
+
+size_t attn_scratch_bytes(int B, int S, int n_kv, int hd) {
+  // RoPE'd K + transposed V, bf16.
+  return (size_t)2 * B * n_kv * S * hd * sizeof(uint16_t);
+}
+
+int launch_attn(const AttnArgs& a, hipStream_t st) {
+  int rc = attn_validate(a.B, a.S, a.n_q, a.n_kv, a.hd);
+  if (rc) return rc;
+  switch (a.hd) {
+    case 64: return launch_attn_hd<64>(a, st);
+    case 96: return launch_attn_hd<96>(a, st);
+    default: return launch_attn_hd<128>(a, st);
+  }
+}
+
+size_t last_attn_scratch_bytes(int B, int S, int n_q, int hd) {
+  return (size_t)B * n_q * (S / LCH) * (hd + 2) * sizeof(float);
+}
+
+int launch_last_attn(const LastAttnArgs& a, hipStream_t st) {
+  int rc = attn_validate(a.B, a.S, a.n_q, a.n_kv, a.hd);
+  if (rc) return rc;
+  MK_REQUIRE(a.S % LCH == 0, "last-token attention: seq must be a multiple of 256");
+  switch (a.hd) {
+    case 64: return launch_last_attn_hd<64>(a, st);
+    case 96: return launch_last_attn_hd<96>(a, st);
+    default: return launch_last_attn_hd<128>(a, st);
+  }
+}
+
+}  // namespace mk

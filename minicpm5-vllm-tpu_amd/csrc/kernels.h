@@ -1,0 +1,117 @@
+// Internal launcher interface between the C ABI / model runner and the HIP kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace mk {
+
+// ------------------------------------------------------------------------------ attention
+struct AttnArgs {
+  const uint16_t* qkv;   // (B, S, (n_q + 2 n_kv) hd) bf16, token-major, [q heads | k heads | v heads]
+  const uint16_t* cos;   // (>= S, hd) bf16 RoPE table
+  const uint16_t* sin;   // (>= S, hd) bf16
+  uint16_t* krope;       // scratch (B, n_kv, S, hd) bf16: RoPE'd K
+  uint16_t* vt;          // scratch (B, n_kv, hd, S) bf16: V transposed
+  uint16_t* out;         // (B, S, n_q hd) bf16
+  int B, S, n_q, n_kv, hd;
+  float qscale;          // multiplies RoPE'd q before the bf16 rounding (sm_scale * log2 e)
+};
+int attn_validate(int B, int S, int n_q, int n_kv, int hd);
+size_t attn_scratch_bytes(int B, int S, int n_kv, int hd);
+int launch_attn(const AttnArgs& a, hipStream_t st);
+
+// Last-token attention of the last layer (mk_jax.py:492-520): one query per sequence over all S keys.
+struct LastAttnArgs {
+  const uint16_t* q;      // (B, n_q, hd) bf16, pre-RoPE (row of the q projection of the last token)
+  const uint16_t* kv;     // (B, S, 2 kv_dim) bf16, pre-RoPE k heads then v heads
+  const uint16_t* cos;    // (>= S, hd)
+  const uint16_t* sin;
+  float* part;            // scratch: (B, n_q, nchunk, hd + 2) f32 partial (m, l, o)
+  uint16_t* out;          // (B, n_q hd) bf16
+  int B, S, n_q, n_kv, hd;
+};
+size_t last_attn_scratch_bytes(int B, int S, int n_q, int hd);
+int launch_last_attn(const LastAttnArgs& a, hipStream_t st);
+
+// ------------------------------------------------------------------------------ GEMM
+// C(M, N) = A(M, K) * B(N, K)^T with A and B K-contiguous (row stride lda / ldb elements).
+enum class GemmIn { I8, BF16 };
+enum class Epi {
+  DQ_BF16,        // out = bf16((acc * rs[m]) * cs[n])                      (fused_qkv)
+  DQ_SILU,        // g/u interleaved by 32 columns: h = silu(g) * u, g,u = (acc * rs[m]) * cs[n]
+  DQ_SILU_F32A,   // same, stores f32 h * aux[n'] (input of the int8 down projection)
+  BF16,           // out = bf16(acc)
+  F32,            // out = acc (f32)
+  RES_BF16ADD,    // res = bf16(res + bf16(acc))                           (bf16 O projection)
+  DQ_RES_BF16ADD, // res = bf16(res + bf16((acc * rs[m]) * cs[n]))          (int8d O projection)
+  RES_F32ADD,     // res = bf16(res + acc)                                  (bf16 down projection)
+  DQ2_RES_F32ADD, // res = bf16(res + acc * (rs[m] * cs[n]))                (int8 down projection)
+  I32,            // out = acc (int32, raw accumulator; tests)
+  SILU_BF16,      // g/u interleaved: g, u = bf16(acc [* (rs[m] * cs[n])]); h = bf16(bf16(silu(g)) * u)
+  DQ2_BF16,       // out = bf16(acc * (rs[m] * cs[n]))                     (linear_rmsnorm int8d)
+};
+struct GemmArgs {
+  GemmIn in;
+  Epi epi;
+  const void* A; int lda;
+  const void* B; int ldb;
+  int M, N, K;
+  void* out; int ldo;         // output (bf16 / f32 / i32), unused by the residual epilogues
+  uint16_t* res; int ldr;     // residual stream (in/out) for RES_* epilogues
+  const float* rs;            // per-row scale (tokens)
+  const float* cs;            // per-column scale (output channels)
+  const float* aux;           // DQ_SILU_F32A: per-intermediate-channel factor
+};
+int gemm_validate(const GemmArgs& g);
+int launch_gemm(const GemmArgs& g, hipStream_t st);
+
+// Skinny GEMM for M <= 32 rows (last-token layer, LM head): same math, weights streamed once.
+int launch_gemm_skinny(const GemmArgs& g, hipStream_t st);
+
+// ------------------------------------------------------------------------------ norm / quant
+// Fused RMSNorm statistics + per-token dynamic int8 quantisation (mk_mlp.py:161-168):
+//   rstd = rsqrt(mean(x^2) + eps); u = x * a; s_u = max(amax|u| / 127, 1e-6);
+//   q = round_half_even(u / s_u); sx = s_u * rstd.   `recip` selects u * (1/s_u) (fused kernels)
+//   instead of u / s_u (XLA path).  With norm == false, rstd is 1 (plain dynamic quant, linear()).
+struct QuantArgs {
+  const void* x; int ldx; bool x_f32;
+  const float* a;        // per-channel factor or null (ones)
+  int T, H;
+  float eps;
+  bool norm, recip;
+  int8_t* q; int ldq;
+  float* sx;
+};
+int launch_rowquant(const QuantArgs& a, hipStream_t st);
+
+// out = bf16(x * rsqrt(mean(x^2) + eps)) [* gamma]   (rms_norm_unit, mk_jax.py:32-36)
+int launch_rmsnorm_bf16(const uint16_t* x, int ldx, const uint16_t* gamma, uint16_t* out, int ldo,
+                        int T, int H, float eps, hipStream_t st);
+// x[t] = embed[clamp(ids[t])]
+int launch_embed(const int32_t* ids, const uint16_t* embed, uint16_t* x, int T, int H, int V,
+                 hipStream_t st);
+// rows[b] = x[b * S + S - 1]
+int launch_gather_last(const uint16_t* x, uint16_t* rows, int B, int S, int H, hipStream_t st);
+// h = bf16(bf16(silu(g)) * u) over (B, I) with gu (B, 2, I) bf16 (last layer)
+int launch_silu_mul_bf16(const uint16_t* gu, uint16_t* h, int B, int I, hipStream_t st);
+// x = bf16(x + y) (bf16 residual add)
+int launch_add_bf16(uint16_t* x, const uint16_t* y, size_t n, hipStream_t st);
+// zero fill (graph-safe replacement for memset)
+int launch_zero(void* p, size_t bytes, hipStream_t st);
+
+// ------------------------------------------------------------------------------ weight packing
+// out(N, K) = in(K, N)^T for 1- or 2-byte elements, optionally with a column map (see pack.hip).
+struct PackArgs {
+  const void* in; int ld_in;      // (K rows, ld_in) source, row-major
+  void* out;                      // (N, K) destination, row-major
+  int K, N;
+  int elem;                       // bytes per element (1 or 2)
+  int map;                        // 0: identity, 1: gate/up 32-interleave from chunk layout
+  int ic, inter;                  // map 1 parameters
+};
+int launch_pack(const PackArgs& p, hipStream_t st);
+int launch_pack_scales(const float* in, float* out, int inter, int ic, hipStream_t st);
+
+}  // namespace mk

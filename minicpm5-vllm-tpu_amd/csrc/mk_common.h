@@ -1,0 +1,104 @@
+// Shared device/host helpers for the MiniCPM5 prefill kernels (gfx950 / CDNA4 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+
+#include <string>
+
+namespace mk {
+
+// ---------------------------------------------------------------------------------------------
+// Vector types used as MFMA operands / 16-byte memory transactions.
+// ---------------------------------------------------------------------------------------------
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------------------------------------
+// bf16 <-> f32.  bf16 values live in memory as uint16_t; rounding is round-to-nearest-even,
+// NaN stays NaN (the result torch/JAX produce for `.astype(bfloat16)`).
+// ---------------------------------------------------------------------------------------------
+__host__ __device__ inline float bf2f(uint16_t h) {
+  uint32_t u = static_cast<uint32_t>(h) << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+__host__ __device__ inline uint16_t f2bf(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);  // quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+// Two floats -> packed bf16x2 (low half = a).
+__device__ inline uint32_t pack_bf2(float a, float b) {
+  return static_cast<uint32_t>(f2bf(a)) | (static_cast<uint32_t>(f2bf(b)) << 16);
+}
+
+__device__ inline float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ inline float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+template <typename T>
+__device__ inline T bitcast(const u32x4& v) {
+  T r;
+  static_assert(sizeof(T) == 16, "16-byte operand");
+  __builtin_memcpy(&r, &v, 16);
+  return r;
+}
+
+// ---------------------------------------------------------------------------------------------
+// MFMA wrappers (gfx950).  32x32 tiles: A operand lane l holds row (l % 32) and 16 bytes of the
+// contraction dim; B operand lane l holds column (l % 32) and the same 16 bytes' worth of k.  The
+// k order inside one instruction is irrelevant as long as A and B use the same lane split.  The
+// accumulator of a 32x32 tile: lane l holds column (l % 32), rows 8*i + 4*(l / 32) + j in
+// register 4*i + j.
+// ---------------------------------------------------------------------------------------------
+__device__ inline f32x16 mfma_bf16_32x32x16(const u32x4& a, const u32x4& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(bitcast<bf16x8>(a), bitcast<bf16x8>(b), c, 0, 0, 0);
+}
+
+__device__ inline i32x16 mfma_i8_32x32x32(const u32x4& a, const u32x4& b, const i32x16& c) {
+  return __builtin_amdgcn_mfma_i32_32x32x32_i8(bitcast<i32x4>(a), bitcast<i32x4>(b), c, 0, 0, 0);
+}
+
+__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// ---------------------------------------------------------------------------------------------
+// Error reporting shared by every launcher: a thread-local message the C ABI hands out.
+// ---------------------------------------------------------------------------------------------
+void set_error(const std::string& msg);
+
+}  // namespace mk
+
+// Status codes of the C ABI.
+#define MK_OK 0
+#define MK_EINVAL -1
+#define MK_EHIP -2
+#define MK_EUNSUPPORTED -3
+#define MK_ENOMEM -4
+
+#define MK_HIP_CHECK(expr)                                                          \
+  do {                                                                              \
+    hipError_t _e = (expr);                                                         \
+    if (_e != hipSuccess) {                                                         \
+      mk::set_error(std::string(#expr) + ": " + hipGetErrorString(_e));             \
+      return MK_EHIP;                                                               \
+    }                                                                               \
+  } while (0)
+
+#define MK_REQUIRE(cond, msg)                                                       \
+  do {                                                                              \
+    if (!(cond)) {                                                                  \
+      mk::set_error(std::string(msg));                                              \
+      return MK_EINVAL;                                                             \
+    }                                                                               \
+  } while (0)

@@ -1,0 +1,67 @@
+// Model runner state (host side of libmk).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <vector>
+
+#include "mk.h"
+
+namespace mk {
+
+// Per-linear precision + flags of a quant string (mk_jax.py:302-318).
+struct QuantPlan {
+  bool i8[4];       // qkv, o, gu, down: int8 weights + per-token dynamic int8 activations
+  bool sq, lastbf16, fqkv, fmlp;
+};
+
+// Byte offsets of the packed (K-contiguous) weights inside the caller's packed buffer.
+struct PackedLayout {
+  size_t wqkv, wo, wgu, sgu, wd, wlqkv, wlo, wlgu, wld, total;
+};
+
+// Byte offsets of the forward's buffers inside the caller's workspace.
+struct WorkLayout {
+  size_t x, xq, sx, qkv, attn, xn, h, att, part, xnl, ql, attl, xl, gul, hl, total;
+};
+
+struct GraphKey {
+  int bs, seq;
+  const void* ids;
+  const void* hidden;
+  const void* logits;
+  const void* ws;
+  bool operator==(const GraphKey& o) const {
+    return bs == o.bs && seq == o.seq && ids == o.ids && hidden == o.hidden && logits == o.logits && ws == o.ws;
+  }
+};
+
+struct CachedGraph {
+  GraphKey key;
+  hipGraphExec_t exec;
+};
+
+struct Model {
+  static constexpr size_t kMaxGraphs = 16;
+  mk_config cfg{};
+  QuantPlan q{};
+  mk_weights w{};
+  PackedLayout P{};
+  char* packed = nullptr;
+  bool use_graph = true;
+  hipStream_t cap_stream = nullptr;
+  std::vector<CachedGraph> graphs;
+  ~Model();
+};
+
+int parse_quant(const char* quant, QuantPlan* p);
+int validate_config(const mk_config* c);
+int validate_run(const mk_config& c, int bs, int seq);
+int packed_layout(const mk_config* c, const QuantPlan& q, PackedLayout* L);
+int workspace_layout(const Model& m, int B, int S, WorkLayout* W);
+int model_create(const mk_config* cfg, const char* quant, const mk_weights* w, void* packed, size_t packed_bytes,
+                 hipStream_t st, Model** out);
+int model_forward(Model* m, const int32_t* ids, int bs, int seq, void* hidden, float* logits, void* ws,
+                  size_t ws_bytes, hipStream_t st);
+
+}  // namespace mk

@@ -1,0 +1,215 @@
+// HBM-bound row kernels: RMSNorm + dynamic int8 quantisation, bf16 RMSNorm, embedding gather and
+// small elementwise ops of the last-token layer (gfx950).  One wave per token row; rows are read
+// with 16-byte vector loads.
+#include "kernels.h"
+#include "mk_common.h"
+
+namespace mk {
+
+namespace {
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ inline float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+template <bool F32>
+__device__ inline void load8(const void* x, size_t off, float v[8]) {
+  if constexpr (F32) {
+    const f32x4* p = reinterpret_cast<const f32x4*>(static_cast<const float*>(x) + off);
+    const f32x4 a = p[0], b = p[1];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { v[e] = a[e]; v[4 + e] = b[e]; }
+  } else {
+    const u32x4 r = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(x) + off);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { v[2 * e] = bf_lo(r[e]); v[2 * e + 1] = bf_hi(r[e]); }
+  }
+}
+
+// Reference algebra: mk_mlp.py:161-168 (fused kernels, recip == true) and
+// mk_jax.py:257-262 / :283-286 (XLA linear / linear_rmsnorm, recip == false).
+template <bool F32>
+__global__ __launch_bounds__(256) void rowquant_kernel(QuantArgs a) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= a.T) return;
+  const int nc = a.H / 8;
+  const size_t xo = (size_t)row * a.ldx;
+  float ss = 0.f, am = 0.f;
+  for (int c = lane; c < nc; c += 64) {
+    float v[8];
+    load8<F32>(a.x, xo + 8 * c, v);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      ss += v[e] * v[e];
+      const float u = a.a ? v[e] * a.a[8 * c + e] : v[e];
+      am = fmaxf(am, fabsf(u));
+    }
+  }
+  ss = wave_sum(ss);
+  am = wave_max(am);
+  const float rstd = a.norm ? 1.f / sqrtf(ss / (float)a.H + a.eps) : 1.f;
+  const float s_u = a.recip ? fmaxf(am * (1.0f / 127.0f), 1e-6f) : fmaxf(am / 127.0f, 1e-6f);
+  const float inv = 1.f / s_u;
+  int8_t* qrow = a.q + (size_t)row * a.ldq;
+  for (int c = lane; c < nc; c += 64) {
+    float v[8];
+    load8<F32>(a.x, xo + 8 * c, v);
+    uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float u = a.a ? v[e] * a.a[8 * c + e] : v[e];
+      float q = a.recip ? rintf(u * inv) : rintf(u / s_u);
+      q = fminf(fmaxf(q, -127.f), 127.f);
+      const uint32_t b = static_cast<uint32_t>(static_cast<int32_t>(q)) & 0xffu;
+      if (e < 4) w0 |= b << (8 * e);
+      else w1 |= b << (8 * (e - 4));
+    }
+    *reinterpret_cast<u32x2*>(qrow + 8 * c) = u32x2{w0, w1};
+  }
+  if (lane == 0) a.sx[row] = s_u * rstd;
+}
+
+__global__ __launch_bounds__(256) void rmsnorm_bf16_kernel(const uint16_t* __restrict__ x, int ldx,
+                                                           const uint16_t* __restrict__ gamma,
+                                                           uint16_t* __restrict__ out, int ldo, int T,
+                                                           int H, float eps) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= T) return;
+  const int nc = H / 8;
+  const uint16_t* xr = x + (size_t)row * ldx;
+  float ss = 0.f;
+  for (int c = lane; c < nc; c += 64) {
+    float v[8];
+    load8<false>(xr, 8 * c, v);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
+  }
+  ss = wave_sum(ss);
+  const float rstd = 1.f / sqrtf(ss / (float)H + eps);
+  uint16_t* orow = out + (size_t)row * ldo;
+  for (int c = lane; c < nc; c += 64) {
+    float v[8];
+    load8<false>(xr, 8 * c, v);
+    u32x4 r;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float a0 = bf2f(f2bf(v[2 * e] * rstd)), a1 = bf2f(f2bf(v[2 * e + 1] * rstd));
+      if (gamma) {
+        a0 *= bf2f(gamma[8 * c + 2 * e]);
+        a1 *= bf2f(gamma[8 * c + 2 * e + 1]);
+      }
+      r[e] = pack_bf2(a0, a1);
+    }
+    *reinterpret_cast<u32x4*>(orow + 8 * c) = r;
+  }
+}
+
+__global__ __launch_bounds__(256) void embed_kernel(const int32_t* __restrict__ ids,
+                                                    const uint16_t* __restrict__ embed,
+                                                    uint16_t* __restrict__ x, int T, int H, int V) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= T) return;
+  int id = ids[row];
+  id = id < 0 ? 0 : (id >= V ? V - 1 : id);   // memory safety: out-of-range ids are clamped
+  const u32x4* src = reinterpret_cast<const u32x4*>(embed + (size_t)id * H);
+  u32x4* dst = reinterpret_cast<u32x4*>(x + (size_t)row * H);
+  for (int c = lane; c < H / 8; c += 64) dst[c] = src[c];
+}
+
+__global__ void gather_last_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ rows, int S,
+                                   int H) {
+  const int b = blockIdx.x;
+  const u32x4* src = reinterpret_cast<const u32x4*>(x + ((size_t)b * S + S - 1) * H);
+  u32x4* dst = reinterpret_cast<u32x4*>(rows + (size_t)b * H);
+  for (int c = threadIdx.x; c < H / 8; c += blockDim.x) dst[c] = src[c];
+}
+
+__global__ void silu_mul_bf16_kernel(const uint16_t* __restrict__ gu, uint16_t* __restrict__ h, int B,
+                                     int I) {
+  const size_t n = (size_t)B * I;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+    const size_t b = i / I, j = i % I;
+    const float g = bf2f(gu[b * 2 * I + j]);
+    const float u = bf2f(gu[b * 2 * I + I + j]);
+    const float s = bf2f(f2bf(g / (1.f + __expf(-g))));
+    h[i] = f2bf(s * u);
+  }
+}
+
+__global__ void add_bf16_kernel(uint16_t* __restrict__ x, const uint16_t* __restrict__ y, size_t n) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    x[i] = f2bf(bf2f(x[i]) + bf2f(y[i]));
+}
+
+__global__ void zero_kernel(uint32_t* __restrict__ p, size_t nwords) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < nwords; i += (size_t)gridDim.x * blockDim.x)
+    p[i] = 0u;
+}
+
+}  // namespace
+
+int launch_rowquant(const QuantArgs& a, hipStream_t st) {
+  MK_REQUIRE(a.T >= 1 && a.H >= 8 && a.H % 8 == 0, "rowquant: H must be a positive multiple of 8");
+  MK_REQUIRE(a.x && a.q && a.sx, "rowquant: null pointer");
+  MK_REQUIRE(a.ldx >= a.H && a.ldq >= a.H && a.ldx % 8 == 0 && a.ldq % 8 == 0, "rowquant: bad strides");
+  const dim3 grid((a.T + 3) / 4);
+  if (a.x_f32) hipLaunchKernelGGL(rowquant_kernel<true>, grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL(rowquant_kernel<false>, grid, dim3(256), 0, st, a);
+  MK_HIP_CHECK(hipGetLastError());
+  return MK_OK;
+}
+
+int launch_rmsnorm_bf16(const uint16_t* x, int ldx, const uint16_t* gamma, uint16_t* out, int ldo, int T,
+                        int H, float eps, hipStream_t st) {
+  MK_REQUIRE(T >= 1 && H % 8 == 0 && ldx % 8 == 0 && ldo % 8 == 0, "rmsnorm: bad shape");
+  hipLaunchKernelGGL(rmsnorm_bf16_kernel, dim3((T + 3) / 4), dim3(256), 0, st, x, ldx, gamma, out, ldo, T, H, eps);
+  MK_HIP_CHECK(hipGetLastError());
+  return MK_OK;
+}
+
+int launch_embed(const int32_t* ids, const uint16_t* embed, uint16_t* x, int T, int H, int V, hipStream_t st) {
+  MK_REQUIRE(T >= 1 && H % 8 == 0 && V >= 1, "embed: bad shape");
+  hipLaunchKernelGGL(embed_kernel, dim3((T + 3) / 4), dim3(256), 0, st, ids, embed, x, T, H, V);
+  MK_HIP_CHECK(hipGetLastError());
+  return MK_OK;
+}
+
+int launch_gather_last(const uint16_t* x, uint16_t* rows, int B, int S, int H, hipStream_t st) {
+  MK_REQUIRE(B >= 1 && S >= 1 && H % 8 == 0, "gather_last: bad shape");
+  hipLaunchKernelGGL(gather_last_kernel, dim3(B), dim3(256), 0, st, x, rows, S, H);
+  MK_HIP_CHECK(hipGetLastError());
+  return MK_OK;
+}
+
+int launch_silu_mul_bf16(const uint16_t* gu, uint16_t* h, int B, int I, hipStream_t st) {
+  const size_t n = (size_t)B * I;
+  const int blocks = (int)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
+  hipLaunchKernelGGL(silu_mul_bf16_kernel, dim3(blocks), dim3(256), 0, st, gu, h, B, I);
+  MK_HIP_CHECK(hipGetLastError());
+  return MK_OK;
+}
+
+int launch_add_bf16(uint16_t* x, const uint16_t* y, size_t n, hipStream_t st) {
+  const int blocks = (int)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
+  hipLaunchKernelGGL(add_bf16_kernel, dim3(blocks), dim3(256), 0, st, x, y, n);
+  MK_HIP_CHECK(hipGetLastError());
+  return MK_OK;
+}
+
+int launch_zero(void* p, size_t bytes, hipStream_t st) {
+  MK_REQUIRE(bytes % 4 == 0 && ((uintptr_t)p % 4) == 0, "zero: size and pointer must be 4-byte multiples");
+  const size_t nw = bytes / 4;
+  const int blocks = (int)((nw + 255) / 256 < 4096 ? (nw + 255) / 256 : 4096);
+  if (nw) hipLaunchKernelGGL(zero_kernel, dim3(blocks), dim3(256), 0, st, static_cast<uint32_t*>(p), nw);
+  MK_HIP_CHECK(hipGetLastError());
+  return MK_OK;
+}
+
+}  // namespace mk

@@ -1,0 +1,259 @@
+"""CPU emulator of the plugin's quantized prefill numerics -- the oracle's per-kernel half.
+
+TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).
+
+Each function restates one piece of the reference's device program on the CPU (torch, f32 unless
+stated), with the reference's rounding points:
+  row_quant        mk_mlp.py:161-168 (fused: u * (1/s)), mk_jax.py:257-262 / :283-286 (XLA: u / s)
+  int_matmul       exact int8 x int8 -> int64 (the MXU / MFMA int32 accumulation is exact)
+  fused_qkv        mk_mlp.py:161-170
+  linear           mk_jax.py:233-269 (bf16 and int8d)
+  linear_rmsnorm   mk_jax.py:272-299 (bf16 and int8d)
+  fused_mlp        mk_mlp.py:68-97 (bf16 and int8 W_down)
+  attention        mk_attn.py:557-657 numerics: RoPE'd q * log2(e) (and the softmax scale) rounded
+                   to bf16, RoPE'd k rounded to bf16, scores f32, p = exp2(s - m) rounded to bf16 for
+                   the PV product, row sum accumulated from that bf16 p, output bf16.  The reference
+                   rounds s - m to bf16 before a bf16 exp2 and rounds k's RoPE products to bf16
+                   separately; `ref_numerics=True` reproduces those two TPU-specific roundings.
+  attention_fp32   the FP32 reference attention of the attention-kernel benchmark (RoPE in f32 on
+                   the bf16 inputs, f32 softmax).
+  last_layer_step  mk_jax.py:492-520
+  mk_forward       mk_jax.py:527-569, 608-665 (+ the inherited LM head in f32)
+
+Pinning: see tests/test_oracle_*.py (closed forms, brute force, exact-algebra invariants, and the
+FP32 golden, which is itself checked against transformers' Llama).
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+BF16 = torch.bfloat16
+F32 = torch.float32
+LOG2E = 1.4426950408889634
+
+
+def bf(x: torch.Tensor) -> torch.Tensor:
+    """Round to bf16 (RNE) and back to f32."""
+    return x.to(BF16).to(F32)
+
+
+# ------------------------------------------------------------------------------------------ quant
+def row_quant(x: torch.Tensor, a: torch.Tensor | None, eps: float, norm: bool, recip: bool):
+    """x (T, H) f32 -> (q int8 (T, H), sx f32 (T,)).  sx = s_u * rstd (rstd = 1 without norm)."""
+    x = x.to(F32)
+    rstd = torch.rsqrt((x * x).mean(-1, keepdim=True) + eps) if norm else torch.ones_like(x[:, :1])
+    u = x * a if a is not None else x
+    amax = u.abs().amax(-1, keepdim=True)
+    if recip:
+        s = torch.clamp(amax * torch.tensor(1.0 / 127.0, dtype=F32), min=1e-6)
+        q = torch.round(u * (1.0 / s))
+    else:
+        s = torch.clamp(amax / 127.0, min=1e-6)
+        q = torch.round(u / s)
+    q = torch.clamp(q, -127, 127).to(torch.int8)
+    return q, (s * rstd).squeeze(-1)
+
+
+def int_matmul(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """Exact int8 (M, K) @ int8 (K, N) -> int64, via f32 GEMMs over K-chunks of 512: every partial sum
+    is an integer of magnitude <= 512 * 127 * 127 < 2**24, so each chunk product is exact in f32."""
+    M, K = a.shape
+    out = torch.zeros((M, b.shape[1]), dtype=torch.float64)
+    af, bfl = a.to(F32), b.to(F32)
+    for k0 in range(0, K, 512):
+        out += (af[:, k0:k0 + 512] @ bfl[k0:k0 + 512]).to(torch.float64)
+    return out.to(torch.int64)
+
+
+def fused_qkv(x: torch.Tensor, w: torch.Tensor, s_w: torch.Tensor, a: torch.Tensor, eps: float) -> torch.Tensor:
+    """(T, H) bf16 -> (T, D) bf16 = bf16((acc * (s_u * rstd)) * s_w)."""
+    q, sx = row_quant(x.to(F32), a, eps, norm=True, recip=True)
+    acc = int_matmul(q, w).to(F32)
+    return ((acc * sx[:, None]) * s_w.reshape(1, -1)).to(BF16)
+
+
+def linear(x: torch.Tensor, w: torch.Tensor, s_w, a_x, quant: str) -> torch.Tensor:
+    """bf16: bf16(x @ w) in f32;  int8d: per-token dynamic quant of x * a_x, bf16((acc * s_x) * s_w)."""
+    if quant == "bf16":
+        return (x.to(F32) @ w.to(F32)).to(BF16)
+    if quant == "int8d":
+        q, sx = row_quant(x.to(F32), a_x, 0.0, norm=False, recip=False)
+        acc = int_matmul(q, w).to(F32)
+        return ((acc * sx[:, None]) * s_w.reshape(1, -1)).to(BF16)
+    raise NotImplementedError(quant)
+
+
+def linear_rmsnorm(x: torch.Tensor, w: torch.Tensor, s_w, a_x, eps: float, quant: str) -> torch.Tensor:
+    xf = x.to(F32)
+    if quant == "bf16":
+        rstd = torch.rsqrt((xf * xf).mean(-1, keepdim=True) + eps)
+        return (bf(xf * rstd) @ w.to(F32)).to(BF16)
+    if quant == "int8d":
+        q, sx = row_quant(xf, a_x, eps, norm=True, recip=False)
+        acc = int_matmul(q, w).to(F32)
+        return (acc * (sx[:, None] * s_w.reshape(1, -1))).to(BF16)
+    raise NotImplementedError(quant)
+
+
+def silu_f32(g: torch.Tensor) -> torch.Tensor:
+    return g / (1.0 + torch.exp(-g))
+
+
+def fused_mlp(x: torch.Tensor, w_gu_il: torch.Tensor, s_gu_il: torch.Tensor, a_gu: torch.Tensor, w_down,
+              s_down, a_down, eps: float, ic: int) -> torch.Tensor:
+    """x + down(silu(g) * u) with chunk-interleaved W_gu (H, 2I) and bf16 or int8 W_down (mk_mlp.py:68-97)."""
+    xf = x.to(F32)
+    q, sx = row_quant(xf, a_gu, eps, norm=True, recip=True)
+    inter = w_gu_il.shape[1] // 2
+    n = inter // ic
+    gu = (int_matmul(q, w_gu_il).to(F32) * sx[:, None]) * s_gu_il.reshape(1, -1)
+    gu = gu.view(-1, n, 2, ic)
+    h = (silu_f32(gu[:, :, 0]) * gu[:, :, 1]).reshape(-1, inter)
+    if w_down.dtype == torch.int8:
+        hs = h * a_down.reshape(1, -1)
+        hq, s_h = row_quant(hs, None, 0.0, norm=False, recip=True)
+        acc = int_matmul(hq, w_down).to(F32) * (s_h[:, None] * s_down.reshape(1, -1))
+    else:
+        acc = bf(h) @ w_down.to(F32)
+    return (xf + acc).to(BF16)
+
+
+# ------------------------------------------------------------------------------------------ RoPE
+def rope_f32(x: torch.Tensor, c: torch.Tensor, s: torch.Tensor) -> torch.Tensor:
+    """Rotate-half RoPE in f32; x (..., S, N, hd), c / s (S, hd) f32."""
+    h = x.shape[-1] // 2
+    rot = torch.cat([-x[..., h:], x[..., :h]], dim=-1)
+    return x * c[:, None, :] + rot * s[:, None, :]
+
+
+# ------------------------------------------------------------------------------------------ attention
+def attention_fp32(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, n_q: int, n_kv: int, hd: int,
+                   sm_scale: float, chunk: int = 512) -> torch.Tensor:
+    """Causal GQA attention in f32: qkv (B, S, D) (bf16 values) -> (B, S, n_q hd) f32."""
+    B, S, _ = qkv.shape
+    g = n_q // n_kv
+    c, s = cos[:S].to(F32), sin[:S].to(F32)
+    out = torch.empty((B, S, n_q * hd), dtype=F32)
+    for b in range(B):
+        x = qkv[b].to(F32).view(S, n_q + 2 * n_kv, hd)
+        q = rope_f32(x[:, :n_q], c, s)
+        k = rope_f32(x[:, n_q:n_q + n_kv], c, s)
+        v = x[:, n_q + n_kv:]
+        for q0 in range(0, S, chunk):
+            q1 = min(S, q0 + chunk)
+            qg = q[q0:q1].view(q1 - q0, n_kv, g, hd).permute(1, 2, 0, 3).reshape(n_kv, g * (q1 - q0), hd)
+            sc = (qg @ k[:q1].permute(1, 2, 0)).view(n_kv, g, q1 - q0, q1) * sm_scale
+            mask = torch.arange(q1)[None, :] > torch.arange(q0, q1)[:, None]
+            sc.masked_fill_(mask, float("-inf"))
+            p = torch.softmax(sc, -1).view(n_kv, g * (q1 - q0), q1)
+            o = (p @ v[:q1].permute(1, 0, 2)).view(n_kv, g, q1 - q0, hd).permute(2, 0, 1, 3)
+            out[b, q0:q1] = o.reshape(q1 - q0, n_q * hd)
+    return out
+
+
+def attention(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, n_q: int, n_kv: int, hd: int,
+              sm_scale: float = 1.0, ref_numerics: bool = False, chunk: int = 512) -> torch.Tensor:
+    """The prefill attention with the plugin's rounding points (module docstring) -> bf16."""
+    B, S, _ = qkv.shape
+    g = n_q // n_kv
+    cb, sb = cos[:S].to(F32), sin[:S].to(F32)
+    out = torch.empty((B, S, n_q * hd), dtype=BF16)
+    for b in range(B):
+        x = qkv[b].to(F32).view(S, n_q + 2 * n_kv, hd)
+        q = bf(rope_f32(x[:, :n_q], cb, sb) * (LOG2E * sm_scale))
+        kr = x[:, n_q:n_q + n_kv]
+        if ref_numerics:   # mk_attn.py:572-575: kr*c + bf16(k_rot)*s with bf16 products and sum
+            h = hd // 2
+            rot = torch.cat([-kr[..., h:], kr[..., :h]], dim=-1)
+            k = bf(bf(kr * cb[:, None]) + bf(rot * sb[:, None]))
+        else:
+            k = bf(rope_f32(kr, cb, sb))
+        v = x[:, n_q + n_kv:]
+        for q0 in range(0, S, chunk):
+            q1 = min(S, q0 + chunk)
+            qg = q[q0:q1].view(q1 - q0, n_kv, g, hd).permute(1, 2, 0, 3).reshape(n_kv, g * (q1 - q0), hd)
+            sc = (qg @ k[:q1].permute(1, 2, 0)).view(n_kv, g, q1 - q0, q1)
+            mask = torch.arange(q1)[None, :] > torch.arange(q0, q1)[:, None]
+            sc.masked_fill_(mask, float("-inf"))
+            m = sc.amax(-1, keepdim=True)
+            z = sc - m
+            p = bf(torch.exp2(bf(z))) if ref_numerics else bf(torch.exp2(z))
+            l = p.sum(-1, keepdim=True)
+            o = (p.view(n_kv, g * (q1 - q0), q1) @ v[:q1].permute(1, 0, 2)).view(n_kv, g, q1 - q0, hd)
+            o = o / l
+            out[b, q0:q1] = o.permute(2, 0, 1, 3).reshape(q1 - q0, n_q * hd).to(BF16)
+    return out
+
+
+# ------------------------------------------------------------------------------------------ model
+def _rms_unit_bf16(x: torch.Tensor, eps: float) -> torch.Tensor:
+    xf = x.to(F32)
+    return bf(xf * torch.rsqrt((xf * xf).mean(-1, keepdim=True) + eps))
+
+
+def last_layer_step(x: torch.Tensor, w: dict, cos, sin, n_q: int, n_kv: int, hd: int, eps: float) -> torch.Tensor:
+    """x (B, S, H) bf16 -> (B, H) bf16: last layer for the last token only, bf16 weights (mk_jax.py:492-520).
+    RoPE results are rounded to bf16 (apply_rope_4d returns bf16); softmax f32 (p not rounded)."""
+    B, S, H = x.shape
+    g = n_q // n_kv
+    qd, kvd = n_q * hd, n_kv * hd
+    xn = _rms_unit_bf16(x, eps)                                            # (B, S, H)
+    wqkv = w["wl_qkv"].to(F32)
+    q_last = (xn[:, -1] @ wqkv[:, :qd]).to(BF16).to(F32).view(B, 1, n_q, hd)
+    kv = (xn.reshape(B * S, H) @ wqkv[:, qd:]).to(BF16).to(F32).view(B, S, 2 * kvd)
+    cb, sb = cos[:S].to(F32), sin[:S].to(F32)
+    k = bf(rope_f32(kv[:, :, :kvd].reshape(B, S, n_kv, hd), cb, sb))
+    v = kv[:, :, kvd:].reshape(B, S, n_kv, hd)
+    q = bf(rope_f32(q_last, cb[-1:], sb[-1:])).view(B, n_kv, g, hd)
+    sc = torch.einsum("bngd,bsnd->bngs", q, k)
+    p = torch.softmax(sc, -1)
+    att = torch.einsum("bngs,bsnd->bngd", p, v).reshape(B, qd).to(BF16).to(F32)
+    x_last = bf(x[:, -1].to(F32) + bf(att @ w["wl_o"].to(F32)))
+    xn2 = _rms_unit_bf16(x_last, eps)
+    gu = bf(xn2 @ w["wl_gu"].to(F32).reshape(H, -1)).view(B, 2, -1)
+    hid = bf(bf(silu_f32(gu[:, 0])) * gu[:, 1])
+    return bf(x_last + bf(hid @ w["wl_down"].to(F32))).to(BF16)
+
+
+@torch.no_grad()
+def mk_forward(ids: torch.Tensor, w: dict, embed: torch.Tensor, final_norm: torch.Tensor, cfg, quant: str,
+               lm_head: torch.Tensor | None = None):
+    """ids (B, S) -> (hidden (B, H) bf16, logits (B, V) f32 or None).  `w` is prepare_mk_weights' dict;
+    supports the bf16 / int8d linears with the fused (fqkv, fmlp) or XLA algebra like libmk."""
+    from minicpm5_mk.mk_weights import mlp_chunk
+    from minicpm5_mk.quant import parse_quant, quant_flags
+
+    qm = parse_quant(quant)
+    fl = quant_flags(quant)
+    fqkv = "fqkv" in fl and qm["qkv"] == "int8d"
+    fmlp = "fmlp" in fl and qm["gu"] == "int8d"
+    B, S = ids.shape
+    H, n_q, n_kv, hd, eps = cfg.hidden, cfg.n_q, cfg.n_kv, cfg.head_dim, cfg.eps
+    inter = cfg.inter
+    x = embed[ids.long()].to(BF16).reshape(B * S, H)
+    cos, sin = w["cos"], w["sin"]
+    for l in range(cfg.num_layers - 1):
+        if fqkv:
+            qkv = fused_qkv(x, w["w_qkv"][l], w["s_qkv"][l], w["a_qkv"][l], eps)
+        else:
+            qkv = linear_rmsnorm(x, w["w_qkv"][l], w["s_qkv"][l], w["a_qkv"][l], eps, qm["qkv"])
+        att = attention(qkv.view(B, S, -1), cos, sin, n_q, n_kv, hd).reshape(B * S, -1)
+        o = linear(att, w["w_o"][l], w["s_o"][l], w["a_o"][l], qm["o"])
+        x = bf(x.to(F32) + o.to(F32)).to(BF16)
+        if fmlp:
+            d8 = w["w_down"].dtype == torch.int8
+            x = fused_mlp(x, w["w_gu"][l], w["s_gu"][l], w["a_gu"][l], w["w_down"][l],
+                          w["s_down"][l] if d8 else None, w["a_down"][l] if d8 else None, eps, mlp_chunk(inter))
+        else:
+            wgu = w["w_gu"][l].reshape(H, 2 * inter)
+            sgu = w["s_gu"][l].reshape(-1)
+            gu = linear_rmsnorm(x, wgu, sgu, w["a_gu"][l], eps, qm["gu"]).to(F32).view(-1, 2, inter)
+            hid = bf(bf(silu_f32(gu[:, 0])) * gu[:, 1]).to(BF16)
+            dn = linear(hid, w["w_down"][l], w["s_down"][l], w["a_down"][l], qm["down"])
+            x = bf(x.to(F32) + dn.to(F32)).to(BF16)
+    x_last = last_layer_step(x.view(B, S, H), w, cos, sin, n_q, n_kv, hd, eps)
+    hidden = (_rms_unit_bf16(x_last, eps) * final_norm.to(F32)).to(BF16)
+    logits = hidden.to(F32) @ lm_head.to(F32).t() if lm_head is not None else None
+    return hidden, logits
