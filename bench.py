@@ -1,0 +1,264 @@
+"""Prefill throughput of the MI355X MiniCPM5 path: one JSON line (see --help).
+
+A step is one whole-model prefill of B sequences x 8192 tokens (random-init weights of the named
+architecture, seeded token ids already resident in HBM) through libmk: embedding -> L-1 W8A8 layers ->
+last-token-only last layer -> final norm -> LM head logits, replayed from a captured hipGraph.
+value = B * 8192 / mean step latency (tokens/s); p50 latency uses linear interpolation
+(benchmark/run_benchmark.py:186-194, :437-440 of the reference).
+
+Extra fields:
+  roofline      the attention kernel (dominant kernel of the step) timed alone with HIP events on its
+                launch stream at the step's shape; algorithmic FLOPs = 4 hd n_q S(S+1)/2 per sequence
+                and layer, peak = MI355X dense bf16 2.5 PFLOP/s.
+  kernels       the same for the QKV / gate-up (int8 MFMA, peak 5.0 POP/s) and O / down (bf16) GEMMs.
+  cpu_baseline  the oracle's FP32 CPU forward (oracle/golden.py, a restatement of the reference's
+                FP32 golden) timed on a bounded sample -- the first --cpu-layers layers of one
+                8192-token sequence -- and scaled to the full model (layers + LM head).
+  sweep         with --sweep: tokens/s and p50 at the other (B, 8192) shapes.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [ROOT, os.path.join(ROOT, "minicpm5-vllm-tpu_amd")]
+
+PEAK = {"bf16": 2516.6, "int8": 5033.2, "hbm": 8000.0}   # MI355X dense TFLOP/s, TOP/s; HBM GB/s
+METRIC = "prefill tokens/sec at (B,8192) B=1..32, 1B and 2B arch; p50 ms at (1,8192)"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def pctl(xs, q):
+    xs = sorted(xs)
+    if len(xs) == 1:
+        return xs[0]
+    k = (len(xs) - 1) * q / 100.0
+    f = math.floor(k)
+    c = min(f + 1, len(xs) - 1)
+    return xs[f] + (xs[c] - xs[f]) * (k - f)
+
+
+def flops_reference(cfg, bs, seq):
+    """verify_results.py:131-140: all L layers over the full sequence + causal attention + head."""
+    qkv = cfg.hidden * (cfg.n_q + 2 * cfg.n_kv) * cfg.head_dim
+    o = cfg.n_q * cfg.head_dim * cfg.hidden
+    gu = cfg.hidden * 2 * cfg.inter
+    dn = cfg.inter * cfg.hidden
+    lin = 2 * (qkv + o + gu + dn) * cfg.num_layers * bs * seq
+    attn = cfg.num_layers * bs * 2 * seq * seq * cfg.head_dim * cfg.n_q
+    return lin + attn + 2 * cfg.hidden * cfg.vocab * bs
+
+
+def time_steps(eng, ids, steps, warmup):
+    import torch
+
+    B, S = ids.shape
+    flat = ids.reshape(-1)
+    for _ in range(warmup):
+        eng.model.forward(flat, B, S, logits=True, copy_out=False)
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for a, b in ev:
+        a.record()
+        eng.model.forward(flat, B, S, logits=True, copy_out=False)
+        b.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    lat = [a.elapsed_time(b) for a, b in ev]
+    return wall, lat
+
+
+def kernel_roofline(cfg, B, S, iters=20):
+    """Times the attention kernel and the layer GEMMs alone at the step's shapes (HIP events)."""
+    import ctypes
+
+    import torch
+
+    from minicpm5_mk import _lib
+    from minicpm5_mk.mk_weights import rope_tables
+
+    lib = _lib.load()
+    dev = torch.device("cuda:0")
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    hd, nq, nkv, H, I = cfg.head_dim, cfg.n_q, cfg.n_kv, cfg.hidden, cfg.inter
+    D = (nq + 2 * nkv) * hd
+    g = torch.Generator(device=dev).manual_seed(0)
+    qkv = torch.randn(B, S, D, generator=g, device=dev).to(torch.bfloat16)
+    cos, sin = (t.to(dev) for t in rope_tables(S, hd, cfg.rope_theta))
+    out = torch.empty(B, S, nq * hd, dtype=torch.bfloat16, device=dev)
+    nb = int(lib.mk_attn_scratch_bytes(B, S, nkv, hd))
+    scratch = torch.empty(nb, dtype=torch.uint8, device=dev)
+    ms = ctypes.c_float()
+    P = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else None  # noqa: E731
+    _lib.check(lib.mk_bench_attn(P(qkv), P(cos), P(sin), P(out), P(scratch), nb, B, S, nq, nkv, hd,
+                                 1.0 / math.sqrt(hd), iters, st, ctypes.byref(ms)), "mk_bench_attn")
+    attn_ms = ms.value
+    attn_flop = 4.0 * hd * nq * S * (S + 1) / 2 * B
+    res = {"attention": {"ms": attn_ms, "flop": attn_flop, "tflops": attn_flop / attn_ms / 1e9,
+                         "peak": PEAK["bf16"]}}
+    del qkv, out, scratch
+    T = B * S
+
+    def bench_gemm(name, is8, epi, M, N, K, silu=False, resid=False):
+        dt = torch.int8 if is8 else torch.bfloat16
+        if is8:
+            A = torch.randint(-127, 128, (M, K), generator=g, device=dev, dtype=torch.int8)
+            Bm = torch.randint(-127, 128, (N, K), generator=g, device=dev, dtype=torch.int8)
+        else:
+            A = torch.randn(M, K, generator=g, device=dev).to(dt)
+            Bm = (torch.randn(N, K, generator=g, device=dev) * 0.02).to(dt)
+        rs = torch.rand(M, generator=g, device=dev) * 1e-3
+        cs = torch.rand(N, generator=g, device=dev) * 1e-3
+        nout = N // 2 if silu else N
+        o = None if resid else torch.empty(M, nout, dtype=torch.bfloat16, device=dev)
+        r = torch.zeros(M, N, dtype=torch.bfloat16, device=dev) if resid else None
+        _lib.check(lib.mk_bench_gemm(int(is8), _lib.EPI[epi], P(A), K, P(Bm), K, M, N, K, P(o), nout if o is not None
+                                     else 0, P(r), N if r is not None else 0, P(rs), P(cs), None, iters, st,
+                                     ctypes.byref(ms)), "mk_bench_gemm")
+        fl = 2.0 * M * N * K
+        res[name] = {"ms": ms.value, "flop": fl, "tflops": fl / ms.value / 1e9,
+                     "peak": PEAK["int8" if is8 else "bf16"]}
+
+    bench_gemm("qkv_int8", True, "dq_bf16", T, D, H)
+    bench_gemm("gate_up_int8", True, "dq_silu", T, 2 * I, H, silu=True)
+    bench_gemm("o_bf16", False, "res_bf16add", T, H, nq * hd, resid=True)
+    bench_gemm("down_bf16", False, "res_f32add", T, H, I, resid=True)
+    for v in res.values():
+        v["frac"] = v["tflops"] / v["peak"]
+    return res
+
+
+def cpu_baseline(cfg, n_layers, seq=8192):
+    """The oracle's FP32 forward (restating benchmark/f32_golden.py) on `n_layers` layers of one
+    sequence, scaled to the full model: layers x L / n_layers + the LM head."""
+    import torch
+
+    from minicpm5_mk.synth import random_hf_state_dict, random_token_ids
+    from oracle import golden
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    names = {"model.embed_tokens.weight", "model.norm.weight", "lm_head.weight"}
+    sub = cfg.replace(num_layers=n_layers)
+    for i in range(n_layers):
+        p = f"model.layers.{i}."
+        names |= {p + n for n in ("input_layernorm.weight", "post_attention_layernorm.weight", "self_attn.q_proj.weight",
+                                  "self_attn.k_proj.weight", "self_attn.v_proj.weight", "self_attn.o_proj.weight",
+                                  "mlp.gate_proj.weight", "mlp.up_proj.weight", "mlp.down_proj.weight")}
+    sd = random_hf_state_dict(cfg, names=names)
+    W = golden.load_f32(sd, sub)
+    del sd
+    ids = random_token_ids(1, seq)[0]
+    cos, sin = golden.rope_tables(seq, cfg.head_dim, cfg.rope_theta)
+    t0 = time.perf_counter()
+    golden.forward_one(ids, W, sub, cos, sin)
+    t_sample = time.perf_counter() - t0
+    t_full = t_sample * cfg.num_layers / n_layers
+    return {"value": seq / t_full, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"oracle FP32 forward (oracle/golden.py) of layers 0..{n_layers - 1} + final norm + LM head "
+                      f"of one {seq}-token sequence in {t_sample:.1f}s, scaled x{cfg.num_layers}/{n_layers} "
+                      f"-> {t_full:.1f}s per sequence",
+            "cpu_model": _cpu_model()}
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--arch", default="1b", help="1b (hd 128, reference HF config) | 1b-hd96 | 2b")
+    ap.add_argument("--batch", type=int, default=1)
+    ap.add_argument("--seq", type=int, default=8192)
+    ap.add_argument("--quant", default="auto")
+    ap.add_argument("--sweep", default="", help="extra batch sizes, e.g. 4,8,16,32")
+    ap.add_argument("--cpu-layers", type=int, default=2, help="layers in the CPU-baseline sample (0 = skip)")
+    ap.add_argument("--no-kernels", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported (DP / SP sharding is "
+              "described in DESIGN.md but not built)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from minicpm5_mk.config import preset
+    from minicpm5_mk.engine import MkEngine
+    from minicpm5_mk.synth import random_token_ids
+
+    cfg = preset(args.arch)
+    t0 = time.perf_counter()
+    eng = MkEngine(cfg, quant=args.quant, max_model_len=max(8256, args.seq + 64), log=log)
+    log(f"[bench] engine built in {time.perf_counter() - t0:.1f}s quant={eng.quant}")
+
+    def run(B, steps, warmup):
+        ids = random_token_ids(B, args.seq, seed=1234).to("cuda:0")
+        wall, lat = time_steps(eng, ids, steps, warmup)
+        mean = sum(lat) / len(lat)
+        return {"batch": B, "tokens_per_s": B * args.seq / (mean / 1e3), "mean_ms": mean, "p50_ms": pctl(lat, 50),
+                "p90_ms": pctl(lat, 90), "wall_ms_per_step": wall,
+                "tflops_reference_formula": flops_reference(cfg, B, args.seq) / (mean / 1e3) / 1e12}
+
+    main_run = run(args.batch, args.steps, args.warmup)
+    log(f"[bench] B={args.batch}: {main_run}")
+    sweep = []
+    for b in [int(x) for x in args.sweep.split(",") if x.strip()]:
+        r = run(b, max(3, min(args.steps, int(80 / b))), 1)
+        log(f"[bench] sweep B={b}: {r}")
+        sweep.append(r)
+    eng.model.release_buffers()
+    kern = None if args.no_kernels else kernel_roofline(cfg, args.batch, args.seq)
+    if kern:
+        log(f"[bench] kernels: {json.dumps(kern)}")
+    eng.close()
+    del eng
+    torch.cuda.empty_cache()
+    cpu = cpu_baseline(cfg, args.cpu_layers, args.seq) if args.cpu_layers > 0 else None
+    if cpu:
+        log(f"[bench] cpu baseline: {cpu}")
+
+    out = {
+        "metric": METRIC, "value": round(main_run["tokens_per_s"], 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(main_run["mean_ms"], 4),
+        "p50_ms": round(main_run["p50_ms"], 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8+bf16" if args.quant != "bf16" else "bf16",
+        "data": "synthetic: random-init N(0,0.02) weights (seed 0), token ids U[1000,30000) (seed 1234)",
+        "config": {"workload": f"minicpm5-{args.arch} prefill/scoring ({args.batch},{args.seq}), last-token logits",
+                   "arch": cfg.name, "batch": args.batch, "seq_len": args.seq, "head_dim": cfg.head_dim,
+                   "quant": args.quant, "parallelism": "single GPU"},
+        "tflops_reference_formula": round(main_run["tflops_reference_formula"], 1),
+    }
+    if kern:
+        a = kern["attention"]
+        out["roofline"] = {"bound": "mfma", "achieved": round(a["tflops"], 1), "peak": PEAK["bf16"], "unit": "TFLOP/s",
+                           "frac": round(a["frac"], 4), "traffic": None, "kernel": "attn_fwd_kernel",
+                           "avg_ms": round(a["ms"], 4)}
+        out["kernels"] = {k: {"avg_ms": round(v["ms"], 4), "tflops": round(v["tflops"], 1), "frac": round(v["frac"], 4)}
+                          for k, v in kern.items()}
+    if cpu:
+        out["cpu_baseline"] = cpu
+    if sweep:
+        out["sweep"] = [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()} for r in sweep]
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -164,6 +164,20 @@ int mk_lm_head(const void* hidden, const void* lm_head, int B, int H, int V, flo
 int mk_pack_weight(const void* in, int ld_in, void* out, int K, int N, int elem_bytes, int map, int ic,
                    int inter, void* stream);
 
+/* ---------------------------------------------------------------- benchmark support
+ * No counterpart in the reference (its harness times whole generate() calls, run_benchmark.py:368-466).
+ * Each runs the named kernel `iters` times on `stream` between two hipEvents recorded on that same
+ * stream and returns the average milliseconds per launch; used by bench.py for roofline figures. */
+
+/* The causal attention kernel alone (its K-RoPE / V-transpose prep runs once, untimed). */
+int mk_bench_attn(const void* qkv, const void* cos, const void* sin, void* out, void* scratch, size_t scratch_bytes,
+                  int B, int S, int n_q, int n_kv, int head_dim, float sm_scale, int iters, void* stream,
+                  float* avg_ms);
+/* One mk_gemm configuration (same arguments as mk_gemm). */
+int mk_bench_gemm(int is_int8, int epi, const void* A, int lda, const void* B, int ldb, int M, int N, int K,
+                  void* out, int ldo, void* res, int ldr, const float* rs, const float* cs, const float* aux,
+                  int iters, void* stream, float* avg_ms);
+
 #ifdef __cplusplus
 }
 #endif

@@ -25,6 +25,29 @@ void set_error(const std::string& msg) { g_error = msg; }
     return MK_EINVAL;                                       \
   }
 
+namespace {
+// Runs `launch` iters times between two events on `st`; average ms per launch.
+template <class F>
+int time_launches(F launch, int iters, hipStream_t st, float* avg_ms) {
+  MK_REQUIRE(iters >= 1 && avg_ms != nullptr, "bench: iters must be >= 1 and avg_ms non-null");
+  hipEvent_t e0, e1;
+  MK_HIP_CHECK(hipEventCreate(&e0));
+  MK_HIP_CHECK(hipEventCreate(&e1));
+  int rc = MK_OK;
+  MK_HIP_CHECK(hipEventRecord(e0, st));
+  for (int i = 0; i < iters && rc == MK_OK; ++i) rc = launch();
+  MK_HIP_CHECK(hipEventRecord(e1, st));
+  MK_HIP_CHECK(hipEventSynchronize(e1));
+  float ms = 0.f;
+  MK_HIP_CHECK(hipEventElapsedTime(&ms, e0, e1));
+  hipEventDestroy(e0);
+  hipEventDestroy(e1);
+  if (rc) return rc;
+  *avg_ms = ms / iters;
+  return MK_OK;
+}
+}  // namespace
+
 extern "C" {
 
 const char* mk_last_error(void) { return mk::g_error.c_str(); }
@@ -126,6 +149,41 @@ int mk_attn_prefill(const void* qkv, const void* cos, const void* sin, void* out
   a.hd = head_dim;
   a.qscale = sm_scale * 1.4426950408889634f;
   MK_TRY(mk::launch_attn(a, static_cast<hipStream_t>(stream)));
+}
+
+
+int mk_bench_attn(const void* qkv, const void* cos, const void* sin, void* out, void* scratch, size_t scratch_bytes,
+                  int B, int S, int n_q, int n_kv, int head_dim, float sm_scale, int iters, void* stream,
+                  float* avg_ms) {
+  int rc = mk::attn_validate(B, S, n_q, n_kv, head_dim);
+  if (rc) return rc;
+  MK_REQUIRE(qkv && cos && sin && out && scratch, "bench_attn: null pointer");
+  MK_REQUIRE(scratch_bytes >= mk::attn_scratch_bytes(B, S, n_kv, head_dim), "bench_attn: scratch too small");
+  mk::AttnArgs a{};
+  a.qkv = static_cast<const uint16_t*>(qkv);
+  a.cos = static_cast<const uint16_t*>(cos);
+  a.sin = static_cast<const uint16_t*>(sin);
+  a.krope = static_cast<uint16_t*>(scratch);
+  a.vt = a.krope + (size_t)B * n_kv * S * head_dim;
+  a.out = static_cast<uint16_t*>(out);
+  a.B = B;
+  a.S = S;
+  a.n_q = n_q;
+  a.n_kv = n_kv;
+  a.hd = head_dim;
+  a.qscale = sm_scale * 1.4426950408889634f;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  rc = mk::launch_attn_stages(a, st, 1);
+  if (rc) return rc;
+  return time_launches([&] { return mk::launch_attn_stages(a, st, 2); }, iters, st, avg_ms);
+}
+
+int mk_bench_gemm(int is_int8, int epi, const void* A, int lda, const void* B, int ldb, int M, int N, int K,
+                  void* out, int ldo, void* res, int ldr, const float* rs, const float* cs, const float* aux,
+                  int iters, void* stream, float* avg_ms) {
+  return time_launches(
+      [&] { return mk_gemm(is_int8, epi, A, lda, B, ldb, M, N, K, out, ldo, res, ldr, rs, cs, aux, stream); }, iters,
+      static_cast<hipStream_t>(stream), avg_ms);
 }
 
 int mk_row_quant(const void* x, int x_f32, const float* a, int T, int H, float eps, int norm, int recip,

@@ -274,15 +274,19 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
 }
 
 template <int HD>
-int launch_attn_hd(const AttnArgs& a, hipStream_t st) {
-  const dim3 pg(a.S / 64, a.n_kv, a.B);
-  hipLaunchKernelGGL(attn_prep_kernel<HD>, pg, dim3(256), 0, st, a.qkv, a.cos, a.sin, a.krope, a.vt,
-                     a.S, a.n_q, a.n_kv);
-  MK_HIP_CHECK(hipGetLastError());
-  const dim3 fg(a.S / QT / 2, a.n_kv, a.B);
-  hipLaunchKernelGGL(attn_fwd_kernel<HD>, fg, dim3(NT), 0, st, a.qkv, a.cos, a.sin, a.krope, a.vt,
-                     a.out, a.S, a.n_q, a.n_kv, a.qscale);
-  MK_HIP_CHECK(hipGetLastError());
+int launch_attn_hd(const AttnArgs& a, hipStream_t st, int stages) {
+  if (stages & 1) {
+    const dim3 pg(a.S / 64, a.n_kv, a.B);
+    hipLaunchKernelGGL(attn_prep_kernel<HD>, pg, dim3(256), 0, st, a.qkv, a.cos, a.sin, a.krope, a.vt,
+                       a.S, a.n_q, a.n_kv);
+    MK_HIP_CHECK(hipGetLastError());
+  }
+  if (stages & 2) {
+    const dim3 fg(a.S / QT / 2, a.n_kv, a.B);
+    hipLaunchKernelGGL(attn_fwd_kernel<HD>, fg, dim3(NT), 0, st, a.qkv, a.cos, a.sin, a.krope, a.vt,
+                       a.out, a.S, a.n_q, a.n_kv, a.qscale);
+    MK_HIP_CHECK(hipGetLastError());
+  }
   return MK_OK;
 }
 
@@ -407,15 +411,17 @@ size_t attn_scratch_bytes(int B, int S, int n_kv, int hd) {
   return (size_t)2 * B * n_kv * S * hd * sizeof(uint16_t);
 }
 
-int launch_attn(const AttnArgs& a, hipStream_t st) {
+int launch_attn_stages(const AttnArgs& a, hipStream_t st, int stages) {
   int rc = attn_validate(a.B, a.S, a.n_q, a.n_kv, a.hd);
   if (rc) return rc;
   switch (a.hd) {
-    case 64: return launch_attn_hd<64>(a, st);
-    case 96: return launch_attn_hd<96>(a, st);
-    default: return launch_attn_hd<128>(a, st);
+    case 64: return launch_attn_hd<64>(a, st, stages);
+    case 96: return launch_attn_hd<96>(a, st, stages);
+    default: return launch_attn_hd<128>(a, st, stages);
   }
 }
+
+int launch_attn(const AttnArgs& a, hipStream_t st) { return launch_attn_stages(a, st, 3); }
 
 size_t last_attn_scratch_bytes(int B, int S, int n_q, int hd) {
   return (size_t)B * n_q * (S / LCH) * (hd + 2) * sizeof(float);

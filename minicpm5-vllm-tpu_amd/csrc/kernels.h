@@ -21,6 +21,8 @@ struct AttnArgs {
 int attn_validate(int B, int S, int n_q, int n_kv, int hd);
 size_t attn_scratch_bytes(int B, int S, int n_kv, int hd);
 int launch_attn(const AttnArgs& a, hipStream_t st);
+// stages: 1 = K-RoPE / V-transpose prep, 2 = the attention kernel, 3 = both
+int launch_attn_stages(const AttnArgs& a, hipStream_t st, int stages);
 
 // Last-token attention of the last layer (mk_jax.py:492-520): one query per sequence over all S keys.
 struct LastAttnArgs {

@@ -1,0 +1,196 @@
+"""Offline prefill/scoring engine with the `vllm.LLM(...).generate(..., max_tokens=1)` surface.
+
+vLLM is not part of this image, so `MkEngine` provides the same call shape the reference's users
+write (README.md:253-266, examples/minimal_vllm_inference.py:90-124):
+
+    llm = MkEngine("1b")                                   # or an MkConfig / HF config + state dict
+    outs = llm.generate([{"prompt_token_ids": ids}], SamplingParams(max_tokens=1, temperature=0.0))
+    outs[0].outputs[0].token_ids                            # [next token]
+
+It serves exactly the reference plugin's fast path -- uniform fresh prefills, max_tokens == 1,
+sampling features of `sampling_fast_ok` (minicpm5_mk/__init__.py:10-32) -- and refuses anything
+else with the reference's reason codes (model.py:139-169): ragged, max_tokens,
+unsupported_sampling_feature, seq.  Weights come from an HF-named state dict (a local checkpoint)
+or the deterministic random init of `minicpm5_mk.synth`; they are prepared by `prepare_mk_weights`
+and run through libmk (`MkModel`).
+"""
+from __future__ import annotations
+
+import dataclasses
+import time
+from dataclasses import dataclass, field
+
+import torch
+
+from . import sampling_fast_ok
+from .config import MkConfig, preset
+from .mk_weights import prepare_mk_weights
+from .quant import resolve_quant_pair
+from .runtime import WEIGHT_ORDER, MkModel
+
+BF16 = torch.bfloat16
+
+
+@dataclass
+class SamplingParams:
+    """The subset of vllm.SamplingParams the fast path reads (plus the fields it must see unset)."""
+    max_tokens: int = 1
+    min_tokens: int = 0
+    temperature: float = 0.0
+    top_p: float = 1.0
+    top_k: int = 0
+    seed: int | None = None
+    logprobs: int | None = None
+    detokenize: bool = False
+    skip_clone: bool = False
+    prompt_logprobs: int | None = None
+    presence_penalty: float = 0.0
+    frequency_penalty: float = 0.0
+    repetition_penalty: float = 1.0
+    min_p: float = 0.0
+    logit_bias: dict | None = None
+    allowed_token_ids: list | None = None
+    bad_words: list | None = None
+    structured_outputs: object = None
+    logits_processors: list | None = None
+
+
+@dataclass
+class CompletionOutput:
+    index: int
+    token_ids: list
+    logprobs: list | None = None
+    text: str = ""
+    finish_reason: str = "length"
+
+
+@dataclass
+class RequestOutput:
+    request_id: str
+    prompt_token_ids: list
+    outputs: list = field(default_factory=list)
+    finished: bool = True
+
+
+class NotEligible(RuntimeError):
+    """The request batch needs a path this engine does not serve (reason code in .reason)."""
+
+    def __init__(self, reason: str, msg: str):
+        super().__init__(f"{reason}: {msg}")
+        self.reason = reason
+
+
+def mk_seq_ok(seq: int, max_seq: int) -> bool:
+    """The reference's fast-path length rule (model.py:131-136) intersected with libmk's (seq % 256)."""
+    if seq <= 0 or seq > max_seq:
+        return False
+    ok_ref = seq % 128 == 0 if seq <= 1024 else seq % 1024 == 0
+    return ok_ref and seq % 256 == 0
+
+
+def eligible_batch(prompts, sps, max_seq: int, require_mt1: bool = True):
+    """(bs, seq) iff the batch is one uniform fresh prefill the fast path serves, else NotEligible."""
+    lens = {len(p) for p in prompts}
+    if len(lens) != 1:
+        raise NotEligible("ragged", f"prompt lengths {sorted(lens)} differ")
+    seq = lens.pop()
+    for sp in sps:
+        if require_mt1 and (sp is None or sp.max_tokens != 1):
+            raise NotEligible("max_tokens", "only max_tokens == 1 requests are served")
+        if not sampling_fast_ok(sp):
+            raise NotEligible("unsupported_sampling_feature", "sampling feature outside the fast path")
+    if not mk_seq_ok(seq, max_seq):
+        raise NotEligible("seq", f"seq {seq} not served (multiple of 256 and 1024 above 1024, <= {max_seq})")
+    return len(prompts), seq
+
+
+class MkEngine:
+    def __init__(self, model="1b", quant: str = "auto", state_dict: dict | None = None, weight_seed: int = 0,
+                 max_model_len: int = 8256, device: str = "cuda:0", log=print):
+        t0 = time.perf_counter()
+        self.cfg = preset(model) if isinstance(model, str) else model
+        self.cfg.validate()
+        cfg = self.cfg
+        self.log = log
+        self.device = torch.device(device)
+        self.max_seq = max_model_len
+        self.quant, _ = resolve_quant_pair(quant, cfg.num_layers, 1, cfg.hidden, cfg.inter)
+        if state_dict is None:
+            from .synth import random_hf_state_dict
+            state_dict = random_hf_state_dict(cfg, seed=weight_seed)
+        w = prepare_mk_weights(state_dict, cfg.as_mk_cfg(), self.quant, max_model_len, cfg.bos_token_id, log=log)
+        dev = self.device
+        self.weights = {k: w[k].to(dev) for k in WEIGHT_ORDER}
+        self.cos, self.sin = w["cos"].to(dev), w["sin"].to(dev)
+        self.embed = state_dict["model.embed_tokens.weight"].to(BF16).to(dev)
+        self.final_norm = state_dict["model.norm.weight"].to(BF16).to(dev)
+        lm = state_dict.get("lm_head.weight", state_dict["model.embed_tokens.weight"])
+        self.lm_head = lm.to(BF16).to(dev)
+        self.model = MkModel(self.weights, self.embed, self.cos, self.sin, self.final_norm, self.quant, cfg.n_q,
+                             cfg.n_kv, cfg.head_dim, cfg.eps, lm_head=self.lm_head)
+        self.counts = {"mk": 0}
+        self.status = {"arch": "MiniCPM5MegakernelForCausalLM", "quant": self.quant, "config": cfg.as_mk_cfg(),
+                       "shapes": {}}
+        log(f"[mk] engine ready ({cfg.name}, quant={self.quant}) in {time.perf_counter() - t0:.1f}s")
+
+    # ------------------------------------------------------------------ scoring
+    @torch.no_grad()
+    def logits(self, ids: torch.Tensor) -> torch.Tensor:
+        """ids (B, S) -> last-position logits (B, V) f32 (the timed prefill step)."""
+        B, S = ids.shape
+        if not mk_seq_ok(S, self.max_seq):
+            raise NotEligible("seq", f"seq {S} not served")
+        ids = ids.to(self.device, non_blocking=True)
+        key = f"mk:{B}x{S}"
+        self.counts["mk"] += 1
+        self.counts[key] = self.counts.get(key, 0) + 1
+        self.status["shapes"].setdefault(key, {"mode": "single", "quant": self.quant})
+        _, lg = self.model.forward(ids.reshape(-1), B, S, logits=True, copy_out=False)
+        return lg
+
+    # ------------------------------------------------------------------ vLLM-like generate
+    @torch.no_grad()
+    def generate(self, prompts, sampling_params=None, use_tqdm: bool = False):
+        ps = [p["prompt_token_ids"] if isinstance(p, dict) else list(p) for p in prompts]
+        sps = sampling_params if isinstance(sampling_params, (list, tuple)) else [sampling_params or SamplingParams()] * len(ps)
+        bs, seq = eligible_batch(ps, sps, self.max_seq)
+        ids = torch.tensor(ps, dtype=torch.int32)
+        lg = self.logits(ids).clone()
+        outs = []
+        for b in range(bs):
+            sp = sps[b]
+            row = lg[b]
+            tok = self._sample(row, sp, b)
+            lps = None
+            if sp.logprobs:
+                lp = torch.log_softmax(row, -1)
+                top = torch.topk(lp, int(sp.logprobs))
+                lps = [{int(i): float(v) for i, v in zip(top.indices.tolist(), top.values.tolist())}]
+                lps[0].setdefault(tok, float(lp[tok]))
+            outs.append(RequestOutput(str(b), ps[b], [CompletionOutput(0, [tok], lps)]))
+        return outs
+
+    @staticmethod
+    def _sample(row: torch.Tensor, sp: SamplingParams, b: int) -> int:
+        if not sp.temperature or sp.temperature <= 0:
+            return int(torch.argmax(row))
+        x = row.float() / sp.temperature
+        if sp.top_k and sp.top_k > 0:
+            kth = torch.topk(x, min(sp.top_k, x.numel())).values[-1]
+            x = torch.where(x < kth, torch.full_like(x, float("-inf")), x)
+        p = torch.softmax(x, -1)
+        if sp.top_p < 1.0:
+            srt, idx = torch.sort(p, descending=True)
+            keep = torch.cumsum(srt, 0) - srt < sp.top_p
+            p = torch.zeros_like(p).scatter_(0, idx[keep], srt[keep])
+            p = p / p.sum()
+        g = torch.Generator(device=p.device)
+        g.manual_seed(sp.seed if sp.seed is not None else b)
+        return int(torch.multinomial(p, 1, generator=g))
+
+    def close(self):
+        self.model.close()
+
+
+__all__ = ["MkEngine", "SamplingParams", "RequestOutput", "CompletionOutput", "NotEligible", "mk_seq_ok",
+           "eligible_batch", "dataclasses"]

@@ -1,0 +1,199 @@
+"""The whole-model op: libmk's mk_model_create / mk_forward behind the reference's op signature.
+
+`forward(...)` takes exactly the arguments of the reference's `minicpm5_mk::forward` op
+(plugin/minicpm5_mk/model.py:749-751, weight order :40-41) and returns the same (max(8, bs), H) bf16
+final-normed last-token hidden states (mk_jax.py:624-665).  One `MkModel` (packed weights + cached
+hipGraphs) is kept per weight set, like the reference keeps one compiled program per static
+signature (model.py:54-86).
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+
+import torch
+
+from ._lib import WEIGHT_FIELDS, MkConfig, MkError, MkWeights, check, load
+from .quant import parse_quant, quant_flags, validate_quant
+
+BF16 = torch.bfloat16
+F32 = torch.float32
+
+WEIGHT_ORDER = ("w_qkv", "w_o", "w_gu", "w_down", "s_qkv", "s_o", "s_gu", "s_down",
+                "a_qkv", "a_o", "a_gu", "a_down", "wl_qkv", "wl_o", "wl_gu", "wl_down")
+ATTN_PREFIXES = ("auto", "v2", "super", "flash", "pallas", "splash", "xla")
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def expected_shapes(L: int, H: int, inter: int, n_q: int, n_kv: int, hd: int, quant: str) -> dict:
+    """{name: (shape, dtype)} of the reference-layout tensors (mk_weights.py:126-263) for `quant`."""
+    qm = parse_quant(quant)
+    fl = quant_flags(quant)
+    Lm, qd = L - 1, n_q * hd
+    D = qd + 2 * n_kv * hd
+    i8 = {k: v == "int8d" for k, v in qm.items()}
+    fmlp = "fmlp" in fl and i8["gu"]
+    wt = lambda k: torch.int8 if i8[k] else BF16  # noqa: E731
+    sc = lambda k, n: (Lm, n) if i8[k] else (Lm, 1)  # noqa: E731
+    return {
+        "w_qkv": ((Lm, H, D), wt("qkv")), "w_o": ((Lm, qd, H), wt("o")),
+        "w_gu": ((Lm, H, 2 * inter) if fmlp else (Lm, H, 2, inter), wt("gu")),
+        "w_down": ((Lm, inter, H), wt("down")),
+        "s_qkv": (sc("qkv", D), F32), "s_o": (sc("o", H), F32),
+        "s_gu": (((Lm, 1, 2 * inter) if fmlp else (Lm, 2, inter)) if i8["gu"] else (Lm, 1), F32),
+        "s_down": (sc("down", H), F32),
+        "a_qkv": (sc("qkv", H), F32), "a_o": (sc("o", qd), F32), "a_gu": (sc("gu", H), F32),
+        "a_down": (sc("down", inter), F32),
+        "wl_qkv": ((H, D), BF16), "wl_o": ((qd, H), BF16), "wl_gu": ((H, 2, inter), BF16),
+        "wl_down": ((inter, H), BF16),
+    }
+
+
+class MkModel:
+    """A libmk model over device tensors in the reference layout (kept alive by this object)."""
+
+    def __init__(self, weights: dict, embed: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                 final_norm: torch.Tensor, quant: str, n_q: int, n_kv: int, head_dim: int, eps: float,
+                 lm_head: torch.Tensor | None = None):
+        validate_quant(quant)
+        lib = load()
+        L = int(weights["w_qkv"].shape[0]) + 1
+        V, H = (int(v) for v in embed.shape)
+        inter = int(weights["w_down"].shape[-2])
+        self.dims = dict(L=L, H=H, I=inter, V=V, n_q=n_q, n_kv=n_kv, hd=head_dim, eps=eps)
+        exp = expected_shapes(L, H, inter, n_q, n_kv, head_dim, quant)
+        for k, (shape, dtype) in exp.items():
+            t = weights[k]
+            if tuple(t.shape) != tuple(shape) or t.dtype != dtype:
+                raise MkError(f"{k}: got {tuple(t.shape)} {t.dtype}, expected {shape} {dtype} for quant {quant!r}")
+        others = {"embed": (embed, (V, H), BF16), "final_norm": (final_norm, (H,), BF16),
+                  "cos": (cos, (cos.shape[0], head_dim), BF16), "sin": (sin, (cos.shape[0], head_dim), BF16)}
+        if lm_head is not None:
+            others["lm_head"] = (lm_head, (V, H), BF16)
+        for k, (t, shape, dtype) in others.items():
+            if tuple(t.shape) != tuple(shape) or t.dtype != dtype:
+                raise MkError(f"{k}: got {tuple(t.shape)} {t.dtype}, expected {shape} {dtype}")
+        tensors = dict(weights, embed=embed, cos=cos, sin=sin, final_norm=final_norm, lm_head=lm_head)
+        for k, t in tensors.items():
+            if t is None:
+                continue
+            if not t.is_cuda or not t.is_contiguous():
+                raise MkError(f"{k}: must be a contiguous GPU tensor")
+            if t.data_ptr() % 16:
+                raise MkError(f"{k}: must be 16-byte aligned")
+        self.device = embed.device
+        self.quant = quant
+        self._keep = tensors
+        self.cfg = MkConfig(L, H, inter, n_q, n_kv, head_dim, V, float(eps), int(cos.shape[0]))
+        self._w = MkWeights(*[ctypes.c_void_p(tensors[n].data_ptr()) if tensors.get(n) is not None else None
+                              for n in WEIGHT_FIELDS])
+        nbytes = ctypes.c_size_t()
+        check(lib.mk_packed_bytes(ctypes.byref(self.cfg), quant.encode(), ctypes.byref(nbytes)), "mk_packed_bytes")
+        self.packed = torch.empty(nbytes.value, dtype=torch.uint8, device=self.device)
+        handle = ctypes.c_void_p()
+        check(lib.mk_model_create(ctypes.byref(self.cfg), quant.encode(), ctypes.byref(self._w),
+                                  ctypes.c_void_p(self.packed.data_ptr()), nbytes.value, _stream(),
+                                  ctypes.byref(handle)), "mk_model_create")
+        self._h = handle
+        self._bufs = {}
+        self._lock = threading.Lock()
+
+    @property
+    def has_lm_head(self) -> bool:
+        return self._keep.get("lm_head") is not None
+
+    def set_graph_mode(self, enable: bool) -> None:
+        check(load().mk_set_graph_mode(self._h, int(enable)), "mk_set_graph_mode")
+
+    def workspace_bytes(self, bs: int, seq: int) -> int:
+        n = ctypes.c_size_t()
+        check(load().mk_workspace_bytes(self._h, bs, seq, ctypes.byref(n)), "mk_workspace_bytes")
+        return n.value
+
+    def _buffers(self, bs: int, seq: int, want_logits: bool):
+        key = (bs, seq, want_logits)
+        b = self._bufs.get(key)
+        if b is None:
+            dev, H, V = self.device, self.dims["H"], self.dims["V"]
+            b = {"ws": torch.empty(self.workspace_bytes(bs, seq), dtype=torch.uint8, device=dev),
+                 "ids": torch.empty(bs * seq, dtype=torch.int32, device=dev),
+                 "hidden": torch.empty((max(8, bs), H), dtype=BF16, device=dev),
+                 "logits": torch.empty((bs, V), dtype=F32, device=dev) if want_logits else None}
+            self._bufs[key] = b
+        return b
+
+    def release_buffers(self) -> None:
+        self._bufs.clear()
+
+    def forward(self, input_ids: torch.Tensor, bs: int, seq: int, logits: bool = False, copy_out: bool = True):
+        """input_ids (>= bs*seq,) int32/int64 on the GPU, sequence-major -> hidden (max(8, bs), H) bf16
+        [, logits (bs, V) f32].  With copy_out=False the returned tensors are this model's persistent
+        buffers for (bs, seq) (overwritten by the next call of that shape)."""
+        if logits and not self.has_lm_head:
+            raise MkError("logits requested but the model was built without lm_head")
+        if input_ids.numel() < bs * seq:
+            raise MkError(f"input_ids has {input_ids.numel()} tokens < bs*seq = {bs * seq}")
+        if not input_ids.is_cuda:
+            raise MkError("input_ids must be on the GPU")
+        check(load().mk_validate(ctypes.byref(self.cfg), self.quant.encode(), bs, seq), "mk_validate")
+        with self._lock:
+            b = self._buffers(bs, seq, logits)
+            b["ids"].copy_(input_ids.reshape(-1)[: bs * seq])
+            lg = b["logits"]
+            check(load().mk_forward(self._h, ctypes.c_void_p(b["ids"].data_ptr()), bs, seq,
+                                    ctypes.c_void_p(b["hidden"].data_ptr()),
+                                    ctypes.c_void_p(lg.data_ptr()) if lg is not None else None,
+                                    ctypes.c_void_p(b["ws"].data_ptr()), b["ws"].numel(), _stream()), "mk_forward")
+            hidden = b["hidden"].clone() if copy_out else b["hidden"]
+            if not logits:
+                return hidden
+            return hidden, (lg.clone() if copy_out else lg)
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            load().mk_model_destroy(self._h)
+            self._h = None
+        self._bufs = {}
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # noqa: BLE001  (interpreter shutdown)
+            pass
+
+
+_MODELS: dict = {}
+
+
+def _validate_attn(attn: str) -> None:
+    if not any(attn.startswith(p) for p in ATTN_PREFIXES):
+        raise MkError(f"attn {attn!r}: unknown (auto | v2[:bq,mc] | super... | flash... | splash... | xla)")
+
+
+def forward(input_ids, embed, cos, sin, final_norm, w_qkv, w_o, w_gu, w_down, s_qkv, s_o, s_gu, s_down,
+            a_qkv, a_o, a_gu, a_down, wl_qkv, wl_o, wl_gu, wl_down, bs: int, seq: int, quant: str, n_q: int,
+            n_kv: int, head_dim: int, eps: float, attn: str = "auto") -> torch.Tensor:
+    """The reference's `minicpm5_mk::forward` op (model.py:749-751) on MI355X.
+
+    `attn` selects among the reference's TPU attention variants; every variant names the same
+    causal GQA attention, which libmk runs with its one HIP kernel (the string is validated only)."""
+    _validate_attn(attn)
+    tensors = (embed, cos, sin, final_norm, w_qkv, w_o, w_gu, w_down, s_qkv, s_o, s_gu, s_down,
+               a_qkv, a_o, a_gu, a_down, wl_qkv, wl_o, wl_gu, wl_down)
+    key = (tuple(t.data_ptr() for t in tensors), tuple(tuple(t.shape) for t in tensors), quant, n_q, n_kv,
+           head_dim, float(eps))
+    m = _MODELS.get(key)
+    if m is None:
+        w = dict(zip(WEIGHT_ORDER, (w_qkv, w_o, w_gu, w_down, s_qkv, s_o, s_gu, s_down,
+                                    a_qkv, a_o, a_gu, a_down, wl_qkv, wl_o, wl_gu, wl_down)))
+        m = _MODELS[key] = MkModel(w, embed, cos, sin, final_norm, quant, n_q, n_kv, head_dim, eps)
+    return m.forward(input_ids, bs, seq)
+
+
+def clear_cache() -> None:
+    for m in _MODELS.values():
+        m.close()
+    _MODELS.clear()
