@@ -192,6 +192,8 @@ def main():
     ap.add_argument("--sweep", default="", help="extra batch sizes, e.g. 4,8,16,32")
     ap.add_argument("--cpu-layers", type=int, default=2, help="layers in the CPU-baseline sample (0 = skip)")
     ap.add_argument("--no-kernels", action="store_true")
+    ap.add_argument("--kernels-only", action="store_true",
+                    help="only the per-kernel timing loops + a 256 MiB device copy (rocprofv3 --pmc calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported (DP / SP sharding is "
@@ -205,6 +207,14 @@ def main():
     from minicpm5_mk.synth import random_token_ids
 
     cfg = preset(args.arch)
+    if args.kernels_only:
+        src = torch.ones(64 << 20, dtype=torch.float32, device="cuda:0")   # 256 MiB read + 256 MiB written
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        kern = kernel_roofline(cfg, args.batch, args.seq, iters=max(1, args.steps))
+        print(json.dumps({"kernels": kern, "copy_bytes_each_way": src.numel() * 4}), flush=True)
+        return
     t0 = time.perf_counter()
     eng = MkEngine(cfg, quant=args.quant, max_model_len=max(8256, args.seq + 64), log=log)
     log(f"[bench] engine built in {time.perf_counter() - t0:.1f}s quant={eng.quant}")

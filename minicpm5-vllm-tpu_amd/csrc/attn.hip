@@ -75,6 +75,7 @@ struct AttnSmem {
   static constexpr int VCH = HD * KT / 8;      // 16-byte chunks per V^T tile
   static constexpr int KPT = (KCH + NT - 1) / NT;
   static constexpr int VPT = (VCH + NT - 1) / NT;
+  static_assert(G * QT * (HD * 2 + 16) <= TOTAL, "output staging must fit in the K/V stages");
 };
 
 template <int HD>
@@ -91,7 +92,14 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
   const int col = lane & 31, half = lane >> 5;
-  const int kv = blockIdx.y, b = blockIdx.z;
+  // XCD-aware work mapping: workgroups are dispatched round-robin over the 8 XCDs (each with its
+  // own L2); consecutive logical work items (same sequence and kv head) go to the same XCD so its
+  // L2 serves one kv head's K / V^T stream.
+  const int nblk = gridDim.x * gridDim.y * gridDim.z;
+  const int lid = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+  const int work = (nblk % 8 == 0) ? (lid % 8) * (nblk / 8) + lid / 8 : lid;
+  const int pair = work % gridDim.x;
+  const int kv = (work / gridDim.x) % n_kv, b = work / (gridDim.x * n_kv);
   const int ntiles = S / QT;
   const int D = (n_q + 2 * n_kv) * HD;
   const int head = kv * G + w;
@@ -99,7 +107,7 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
   const uint16_t* vg = vt + ((size_t)b * n_kv + kv) * (size_t)HD * S;
 
   for (int pass = 0; pass < 2; ++pass) {
-    const int qt = pass == 0 ? (int)blockIdx.x : ntiles - 1 - (int)blockIdx.x;
+    const int qt = pass == 0 ? pair : ntiles - 1 - pair;
     const int t0 = qt * QT;
     const int tok = t0 + col;
 
@@ -214,7 +222,13 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[1][r]);
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
       const float mnew = fmaxf(m, mx);
-      const float alpha = fast_exp2(m - mnew);
+      // rescale only when some row max of this wave grew (alpha == 1 exactly otherwise)
+      if (__any(mnew > m)) {
+        const float alpha = fast_exp2(m - mnew);
+        l *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+      }
       m = mnew;
 
       u32x4 pb[2][2];
@@ -229,14 +243,12 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
             const float p0 = fast_exp2(sacc[c][8 * s2 + 2 * e] - mnew);
             const float p1 = fast_exp2(sacc[c][8 * s2 + 2 * e + 1] - mnew);
             const uint32_t pk = pack_bf2(p0, p1);
-            psum += bf_lo(pk) + bf_hi(pk);
+            psum = dot2_bf16_sum(pk, psum);   // row sum of exactly the bf16 P used for PV
             v[e] = pk;
           }
           pb[c][s2] = v;
         }
-      l = l * alpha + psum;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+      l += psum;
 
       // O^T (hd x 32 tokens) += V^T P^T
 #pragma unroll
@@ -260,7 +272,10 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
 
     l += __shfl_xor(l, 32, 64);
     const float inv = 1.f / l;
-    uint16_t* orow = out + ((size_t)b * S + tok) * (size_t)(n_q * HD) + head * HD;
+    // stage this wave's (32 tokens x hd) output tile in LDS (the K/V stages are free after the last
+    // barrier of the loop), then write whole rows with 16-byte stores
+    constexpr int OROW = HD * 2 + 16;
+    char* ot = smem + w * (QT * OROW);
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -268,8 +283,20 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
         const int d0 = dt * 32 + 8 * i + 4 * half;
         u32x2 v = {pack_bf2(o[dt][4 * i] * inv, o[dt][4 * i + 1] * inv),
                    pack_bf2(o[dt][4 * i + 2] * inv, o[dt][4 * i + 3] * inv)};
-        *reinterpret_cast<u32x2*>(orow + d0) = v;
+        *reinterpret_cast<u32x2*>(ot + col * OROW + d0 * 2) = v;
       }
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+    constexpr int OCH = QT * HD / 8;   // 16-byte chunks of the tile
+#pragma unroll
+    for (int i = 0; i < (OCH + 63) / 64; ++i) {
+      const int c = lane + 64 * i;
+      if (c < OCH) {
+        const int r = c / (HD / 8), cc = c % (HD / 8);
+        const u32x4 v = *reinterpret_cast<const u32x4*>(ot + r * OROW + cc * 16);
+        *reinterpret_cast<u32x4*>(out + ((size_t)b * S + t0 + r) * (size_t)(n_q * HD) + head * HD + cc * 8) = v;
+      }
+    }
   }
 }
 

@@ -24,24 +24,23 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // bf16 <-> f32.  bf16 values live in memory as uint16_t; rounding is round-to-nearest-even,
 // NaN stays NaN (the result torch/JAX produce for `.astype(bfloat16)`).
 // ---------------------------------------------------------------------------------------------
-__host__ __device__ inline float bf2f(uint16_t h) {
+__device__ inline float bf2f(uint16_t h) {
   uint32_t u = static_cast<uint32_t>(h) << 16;
   float f;
   memcpy(&f, &u, 4);
   return f;
 }
 
-__host__ __device__ inline uint16_t f2bf(float f) {
-  uint32_t u;
-  memcpy(&u, &f, 4);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);  // quiet NaN
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
-}
+// Hardware conversion (v_cvt_pk_bf16_f32 on gfx950): round-to-nearest-even, NaN -> quiet NaN.
+__device__ inline uint16_t f2bf(float f) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f)); }
 
-// Two floats -> packed bf16x2 (low half = a).
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Two floats -> packed bf16x2 (low half = a), one v_cvt_pk_bf16_f32.
 __device__ inline uint32_t pack_bf2(float a, float b) {
-  return static_cast<uint32_t>(f2bf(a)) | (static_cast<uint32_t>(f2bf(b)) << 16);
+  const f32x2 v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
 
 __device__ inline float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
@@ -71,6 +70,12 @@ __device__ inline i32x16 mfma_i8_32x32x32(const u32x4& a, const u32x4& b, const 
 }
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// acc + lo(w) + hi(w) for a packed bf16 pair (v_dot2_f32_bf16 with (1, 1))
+__device__ inline float dot2_bf16_sum(uint32_t w, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), __builtin_bit_cast(bf16x2, 0x3f803f80u),
+                                          acc, false);
+}
 
 // ---------------------------------------------------------------------------------------------
 // Error reporting shared by every launcher: a thread-local message the C ABI hands out.

@@ -35,21 +35,37 @@ __device__ inline void load8(const void* x, size_t off, float v[8]) {
 
 // Reference algebra: mk_mlp.py:161-168 (fused kernels, recip == true) and
 // mk_jax.py:257-262 / :283-286 (XLA linear / linear_rmsnorm, recip == false).
-template <bool F32>
+// One wave per row; the row stays in registers (NC 8-element chunks per lane, all loads issued
+// before the first use) so the row costs one HBM round trip.
+template <bool F32, int NC>
 __global__ __launch_bounds__(256) void rowquant_kernel(QuantArgs a) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (row >= a.T) return;
   const int nc = a.H / 8;
   const size_t xo = (size_t)row * a.ldx;
-  float ss = 0.f, am = 0.f;
-  for (int c = lane; c < nc; c += 64) {
-    float v[8];
-    load8<F32>(a.x, xo + 8 * c, v);
+  float v[NC][8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      ss += v[e] * v[e];
-      const float u = a.a ? v[e] * a.a[8 * c + e] : v[e];
-      am = fmaxf(am, fabsf(u));
+  for (int i = 0; i < NC; ++i) {
+    const int c = lane + 64 * i;
+    if (c < nc) load8<F32>(a.x, xo + 8 * c, v[i]);
+  }
+  float ss = 0.f, am = 0.f;
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int c = lane + 64 * i;
+    if (c < nc) {
+      f32x4 a0 = {1.f, 1.f, 1.f, 1.f}, a1 = {1.f, 1.f, 1.f, 1.f};
+      if (a.a) {
+        const f32x4* ap = reinterpret_cast<const f32x4*>(a.a + 8 * c);
+        a0 = ap[0];
+        a1 = ap[1];
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        ss += v[i][e] * v[i][e];
+        v[i][e] = a.a ? v[i][e] * (e < 4 ? a0[e] : a1[e - 4]) : v[i][e];   // u = x * a
+        am = fmaxf(am, fabsf(v[i][e]));
+      }
     }
   }
   ss = wave_sum(ss);
@@ -58,14 +74,14 @@ __global__ __launch_bounds__(256) void rowquant_kernel(QuantArgs a) {
   const float s_u = a.recip ? fmaxf(am * (1.0f / 127.0f), 1e-6f) : fmaxf(am / 127.0f, 1e-6f);
   const float inv = 1.f / s_u;
   int8_t* qrow = a.q + (size_t)row * a.ldq;
-  for (int c = lane; c < nc; c += 64) {
-    float v[8];
-    load8<F32>(a.x, xo + 8 * c, v);
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int c = lane + 64 * i;
+    if (c >= nc) continue;
     uint32_t w0 = 0, w1 = 0;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float u = a.a ? v[e] * a.a[8 * c + e] : v[e];
-      float q = a.recip ? rintf(u * inv) : rintf(u / s_u);
+      float q = a.recip ? rintf(v[i][e] * inv) : rintf(v[i][e] / s_u);
       q = fminf(fmaxf(q, -127.f), 127.f);
       const uint32_t b = static_cast<uint32_t>(static_cast<int32_t>(q)) & 0xffu;
       if (e < 4) w0 |= b << (8 * e);
@@ -159,9 +175,24 @@ int launch_rowquant(const QuantArgs& a, hipStream_t st) {
   MK_REQUIRE(a.T >= 1 && a.H >= 8 && a.H % 8 == 0, "rowquant: H must be a positive multiple of 8");
   MK_REQUIRE(a.x && a.q && a.sx, "rowquant: null pointer");
   MK_REQUIRE(a.ldx >= a.H && a.ldq >= a.H && a.ldx % 8 == 0 && a.ldq % 8 == 0, "rowquant: bad strides");
+  MK_REQUIRE(a.H <= 8 * 64 * 16, "rowquant: H must be <= 8192");
+  MK_REQUIRE(((uintptr_t)a.x % 16) == 0 && ((uintptr_t)a.q % 8) == 0 && (!a.a || ((uintptr_t)a.a % 16) == 0),
+             "rowquant: x / a must be 16-byte and q 8-byte aligned");
   const dim3 grid((a.T + 3) / 4);
-  if (a.x_f32) hipLaunchKernelGGL(rowquant_kernel<true>, grid, dim3(256), 0, st, a);
-  else hipLaunchKernelGGL(rowquant_kernel<false>, grid, dim3(256), 0, st, a);
+  const int nc = (a.H / 8 + 63) / 64;   // 8-element chunks per lane
+#define MK_RQ(NC)                                                                                      \
+  if (a.x_f32) hipLaunchKernelGGL((rowquant_kernel<true, NC>), grid, dim3(256), 0, st, a);          \
+  else hipLaunchKernelGGL((rowquant_kernel<false, NC>), grid, dim3(256), 0, st, a);
+  if (nc <= 4) {
+    MK_RQ(4)
+  } else if (nc <= 8) {
+    MK_RQ(8)
+  } else if (nc <= 12) {
+    MK_RQ(12)
+  } else {
+    MK_RQ(16)
+  }
+#undef MK_RQ
   MK_HIP_CHECK(hipGetLastError());
   return MK_OK;
 }
