@@ -1,0 +1,121 @@
+"""The C ABI (include/mk.h) and the host-side plugin surface, without a GPU.
+
+  * libmk.so loads and exports every function include/mk.h declares;
+  * host-only entry points validate like the reference's trace-time asserts and fast-path rules:
+    mk_validate / mk_packed_bytes accept the shapes and quant strings the kernels build and reject the rest
+    with a message (no GPU call);
+  * the packed-weight size matches the layout's arithmetic;
+  * sampling_fast_ok / eligible_batch / mk_seq_ok mirror __init__.py:10-32 and model.py:131-169.
+"""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    src = open(os.path.join(ROOT, "include", "mk.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(mk_[a-z0-9_]+)\s*\(", src)))
+
+
+def test_library_exports_every_declared_symbol():
+    from minicpm5_mk import _lib
+
+    lib = _lib.load()
+    names = _declared()
+    assert len(names) >= 15
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(_lib.SIGNATURES), "ctypes signatures must cover exactly the header"
+    assert lib.mk_abi_version() == 1
+
+
+def _cfg(**kw):
+    from minicpm5_mk import _lib
+
+    d = dict(num_layers=24, hidden=1536, inter=4608, n_q=16, n_kv=2, head_dim=128, vocab=130560, eps=1e-6,
+             max_seq=8256)
+    d.update(kw)
+    return _lib.MkConfig(**d)
+
+
+@pytest.mark.parametrize("kw,quant,bs,seq,code,msg", [
+    ({}, b"int8d:qkv+gu|sq|lastbf16|fqkv|fmlp", 1, 8192, 0, ""),
+    ({}, b"bf16", 32, 8192, 0, ""),
+    ({"head_dim": 96}, b"int8d", 4, 2048, 0, ""),
+    ({}, b"fp8d", 1, 8192, -3, "not built"),
+    ({}, b"int8", 1, 8192, -3, "not built"),
+    ({}, b"int4", 1, 8192, -1, "unknown base"),
+    ({}, b"int8d:qkv+mlp", 1, 8192, -1, "unknown linear"),
+    ({}, b"int8d|fast", 1, 8192, -1, "unknown flag"),
+    ({}, b"bf16", 1, 8000, -1, "multiple of 256"),
+    ({}, b"bf16", 1, 16384, -1, "max_seq"),
+    ({}, b"bf16", 0, 8192, -1, "bs"),
+    ({"n_q": 12}, b"bf16", 1, 8192, -1, "8 * n_kv"),
+    ({"head_dim": 80}, b"bf16", 1, 8192, -1, "head_dim"),
+    ({"hidden": 1000}, b"bf16", 1, 8192, -1, "hidden"),
+    ({"num_layers": 1}, b"bf16", 1, 8192, -1, "num_layers"),
+])
+def test_validate(kw, quant, bs, seq, code, msg):
+    from minicpm5_mk import _lib
+
+    lib = _lib.load()
+    cfg = _cfg(**kw)
+    rc = lib.mk_validate(ctypes.byref(cfg), quant, bs, seq)
+    assert rc == code, lib.mk_last_error()
+    if code:
+        assert msg in lib.mk_last_error().decode()
+
+
+def test_packed_bytes_arithmetic():
+    from minicpm5_mk import _lib
+
+    lib = _lib.load()
+    cfg = _cfg()
+    n = ctypes.c_size_t()
+    assert lib.mk_packed_bytes(ctypes.byref(cfg), b"int8d:qkv+gu|sq|lastbf16|fqkv|fmlp", ctypes.byref(n)) == 0
+    Lm, H, I, D, qd = 23, 1536, 4608, 2560, 2048
+    al = lambda v: (v + 255) // 256 * 256  # noqa: E731
+    exp = (al(Lm * D * H) + al(Lm * H * qd * 2) + al(Lm * 2 * I * H) + al(Lm * 2 * I * 4) + al(Lm * H * I * 2)
+           + al(D * H * 2) + al(H * qd * 2) + al(2 * I * H * 2) + al(H * I * 2))
+    assert n.value == exp
+
+
+def test_sampling_fast_ok_and_eligibility():
+    from minicpm5_mk import sampling_fast_ok
+    from minicpm5_mk.engine import NotEligible, SamplingParams, eligible_batch, mk_seq_ok
+
+    assert sampling_fast_ok(SamplingParams())
+    assert sampling_fast_ok(SamplingParams(temperature=0.7, top_p=0.9, top_k=5, seed=3, logprobs=20))
+    assert not sampling_fast_ok(None)
+    for bad in ({"prompt_logprobs": 1}, {"presence_penalty": 0.1}, {"frequency_penalty": 0.1},
+                {"repetition_penalty": 1.1}, {"min_p": 0.1}, {"logit_bias": {1: 1.0}}, {"allowed_token_ids": [1]},
+                {"bad_words": ["x"]}, {"structured_outputs": object()}, {"logits_processors": [print]}):
+        assert not sampling_fast_ok(SamplingParams(**bad)), bad
+    # the reference rule: <= 1024 -> % 128, else % 1024; libmk adds % 256
+    assert [mk_seq_ok(s, 8256) for s in (128, 256, 768, 1024, 2048, 3072, 8192, 9216, 0)] == \
+        [False, True, True, True, True, True, True, False, False]
+    sp = SamplingParams()
+    assert eligible_batch([[1] * 1024] * 3, [sp] * 3, 8256) == (3, 1024)
+    for prompts, sps, reason in (([[1] * 1024, [1] * 2048], [sp, sp], "ragged"),
+                                 ([[1] * 1024], [SamplingParams(max_tokens=2)], "max_tokens"),
+                                 ([[1] * 1024], [SamplingParams(min_p=0.5)], "unsupported_sampling_feature"),
+                                 ([[1] * 1000], [sp], "seq")):
+        with pytest.raises(NotEligible) as e:
+            eligible_batch(prompts, sps, 8256)
+        assert e.value.reason == reason
+
+
+def test_ops_refuse_cpu_tensors():
+    """The product has no CPU path: kernel wrappers reject host tensors before any launch."""
+    import torch
+
+    from minicpm5_mk import ops
+
+    with pytest.raises(ops.MkError, match="GPU tensor"):
+        ops.attn_prefill(torch.zeros(1, 256, 20 * 64, dtype=torch.bfloat16), torch.zeros(256, 64, dtype=torch.bfloat16),
+                         torch.zeros(256, 64, dtype=torch.bfloat16), 16, 2, 64)

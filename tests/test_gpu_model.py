@@ -4,8 +4,9 @@
     algebra (oracle/emulate.mk_forward) on identical prepared weights and ids.
   * full MiniCPM5 architectures at (1, 8192) with random-init weights (seed 0) and ids (seed 1234),
     auto quant: last-token logits vs the committed FP32 golden (tests/golden/golden_*.npz, written by
-    tests/golden/make_golden.py from oracle/golden.py).  The argmax must be identical; the logits
-    tolerance is stated per config below (about 2x the CPU emulator's own W8A8 error vs FP32).
+    tests/golden/make_golden.py from oracle/golden.py).  The argmax must be identical (tie-aware for the
+    one config whose golden top-2 margin is below the W8A8 error); the logits tolerance is stated per
+    config below (about 2x the CPU emulator's own W8A8 error vs FP32).
   * batch invariance: a sequence scored inside a batch of 4 equals the same sequence alone, bitwise.
   * hipGraph replay equals eager launches, bitwise.
 """
@@ -75,12 +76,19 @@ def test_tiny_vs_emulator(name, quant):
     m.close()
 
 
-# (preset, logits max-abs tolerance vs FP32, mean-abs tolerance)
-FULL = [("1b", 0.25, 0.04), ("1b-hd96", 0.25, 0.04), ("2b", 0.3, 0.05)]
+# (preset, logits max-abs tolerance vs FP32, mean-abs tolerance): 2x the error of the CPU emulation of
+# the same W8A8 numerics (oracle/emulate.mk_forward) vs the FP32 golden at (1, 8192):
+#   1b       max 0.216  mean 0.0359  mean|dlogprob| top-20 0.050
+#   1b-hd96  max 0.262  mean 0.0467                        0.046
+#   2b       max 0.519  mean 0.0923                        0.092   (int8 O projection too)
+# strict: the argmax must equal the golden's.  1b-hd96's golden top-1 / top-2 margin (0.029) is below the
+# W8A8 path's mean logit error, so there the top-1 is judged tie-aware like the reference gate
+# (benchmark/gate.py:47-56): the chosen token must be within 0.1 nats of the golden top-1.
+FULL = [("1b", 0.45, 0.075, True), ("1b-hd96", 0.55, 0.095, False), ("2b", 1.05, 0.19, True)]
 
 
-@pytest.mark.parametrize("name,tol_max,tol_mean", FULL)
-def test_full_model_vs_fp32_golden(name, tol_max, tol_mean):
+@pytest.mark.parametrize("name,tol_max,tol_mean,strict", FULL)
+def test_full_model_vs_fp32_golden(name, tol_max, tol_mean, strict):
     from minicpm5_mk.config import preset
     from minicpm5_mk.quant import resolve_quant_pair
     from minicpm5_mk.synth import random_hf_state_dict, random_token_ids
@@ -108,8 +116,12 @@ def test_full_model_vs_fp32_golden(name, tol_max, tol_mean):
     print(f"[full] {name}: logits max {err.max():.4f} mean {err.mean():.4f} rel {err.max() / g.abs().max():.4f}; "
           f"argmax {int(lg.argmax())} vs {int(g.argmax())} (golden margin {float(srt[0] - srt[1]):.4f}); "
           f"mean |dlogprob| top20 {float(dlp):.4f}", flush=True)
-    assert int(lg.argmax()) == int(g.argmax())
+    if strict:
+        assert int(lg.argmax()) == int(g.argmax())
+    else:
+        assert float(lpg.max() - lpg[int(lg.argmax())]) <= 0.1
     assert err.max() <= tol_max and err.mean() <= tol_mean
+    assert float(dlp) <= 0.15            # the reference gate's FAIL boundary (benchmark/gate.py:115)
     m.close()
 
 
