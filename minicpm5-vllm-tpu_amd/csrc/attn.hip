@@ -65,18 +65,24 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(const uint16_t* __restri
 
 template <int HD>
 struct AttnSmem {
-  static constexpr int KROW = HD * 2 + 16;   // bytes per K row (padded)
-  static constexpr int VROW = KT * 2 + 16;   // bytes per V^T row (padded)
+  static constexpr int KROW = HD * 2 + 16;   // bytes per K row (padded: conflict-free 16-byte reads)
+  static constexpr int VROW = KT * 2 + 8;    // bytes per V^T row: 136 = 8 (mod 256) -> 8-byte reads of
+                                             // 32 consecutive rows hit distinct banks
   static constexpr int KBYTES = KT * KROW;
   static constexpr int VBYTES = HD * VROW;
-  static constexpr int STAGE = KBYTES + VBYTES;
-  static constexpr int TOTAL = 2 * STAGE;
-  static constexpr int KCH = KT * HD / 8;      // 16-byte chunks per K tile
-  static constexpr int VCH = HD * KT / 8;      // 16-byte chunks per V^T tile
+  static constexpr int NK = 3, NV = 2;       // K ring (QK runs one tile ahead), V ring
+  static constexpr int TOTAL = NK * KBYTES + NV * VBYTES;
+  static constexpr int KCH = KT * HD / 8;    // 16-byte chunks per K tile
+  static constexpr int VCH = HD * KT / 8;    // 16-byte chunks per V^T tile
   static constexpr int KPT = (KCH + NT - 1) / NT;
   static constexpr int VPT = (VCH + NT - 1) / NT;
-  static_assert(G * QT * (HD * 2 + 16) <= TOTAL, "output staging must fit in the K/V stages");
+  static_assert(G * QT * (HD * 2 + 16) <= TOTAL, "output staging must fit in the K/V rings");
 };
+
+// Online softmax keeps a per-row reference max m and rescales O / l only when a row max exceeds
+// it by more than RESCALE_T (log2 units): p = exp2(s - m) <= 2^8 stays exact in f32 and in bf16's
+// relative precision, and O / l is unchanged by the choice of m.
+constexpr float RESCALE_T = 8.f;
 
 template <int HD>
 __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
@@ -88,6 +94,8 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
   constexpr int KS = HD / 16;   // k-steps of QK^T
   constexpr int DT = HD / 32;   // 32-row d tiles of O^T
   __shared__ __attribute__((aligned(16))) char smem[L::TOTAL];
+  char* const kring = smem;
+  char* const vring = smem + L::NK * L::KBYTES;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
@@ -105,6 +113,52 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
   const int head = kv * G + w;
   const uint16_t* kg = krope + ((size_t)b * n_kv + kv) * (size_t)S * HD;
   const uint16_t* vg = vt + ((size_t)b * n_kv + kv) * (size_t)HD * S;
+
+  u32x4 kst[L::KPT], vst[L::VPT];
+  auto gload_k = [&](int kt) {
+#pragma unroll
+    for (int i = 0; i < L::KPT; ++i) {
+      const int c = tid + i * NT;
+      if (L::KCH % NT == 0 || c < L::KCH) {
+        const int key = c / (HD / 8), dc = c % (HD / 8);
+        kst[i] = *reinterpret_cast<const u32x4*>(kg + (size_t)(kt * KT + key) * HD + dc * 8);
+      }
+    }
+  };
+  auto gload_v = [&](int kt) {
+#pragma unroll
+    for (int i = 0; i < L::VPT; ++i) {
+      const int c = tid + i * NT;
+      if (L::VCH % NT == 0 || c < L::VCH) {
+        const int d = c / (KT / 8), kc = c % (KT / 8);
+        vst[i] = *reinterpret_cast<const u32x4*>(vg + (size_t)d * S + kt * KT + kc * 8);
+      }
+    }
+  };
+  auto sstore_k = [&](int slot) {
+    char* ks = kring + slot * L::KBYTES;
+#pragma unroll
+    for (int i = 0; i < L::KPT; ++i) {
+      const int c = tid + i * NT;
+      if (L::KCH % NT == 0 || c < L::KCH) {
+        const int key = c / (HD / 8), dc = c % (HD / 8);
+        *reinterpret_cast<u32x4*>(ks + key * L::KROW + dc * 16) = kst[i];
+      }
+    }
+  };
+  auto sstore_v = [&](int slot) {
+    char* vs = vring + slot * L::VBYTES;
+#pragma unroll
+    for (int i = 0; i < L::VPT; ++i) {
+      const int c = tid + i * NT;
+      if (L::VCH % NT == 0 || c < L::VCH) {
+        const int d = c / (KT / 8), kc = c % (KT / 8);
+        u32x2* dst = reinterpret_cast<u32x2*>(vs + d * L::VROW + kc * 16);   // 8-byte aligned rows
+        dst[0] = u32x2{vst[i][0], vst[i][1]};
+        dst[1] = u32x2{vst[i][2], vst[i][3]};
+      }
+    }
+  };
 
   for (int pass = 0; pass < 2; ++pass) {
     const int qt = pass == 0 ? pair : ntiles - 1 - pair;
@@ -139,74 +193,29 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
       }
     }
 
-    const int nkt = (t0 + QT - 1) / KT + 1;
+    const int nkt = (t0 + QT - 1) / KT + 1;   // key tiles 0 .. nkt-1 (the last one crosses the diagonal)
     f32x16 o[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) o[dt] = f32x16{};
     float m = -INFINITY, l = 0.f;
 
-    u32x4 kst[L::KPT], vst[L::VPT];
-    auto gload = [&](int kt) {
-#pragma unroll
-      for (int i = 0; i < L::KPT; ++i) {
-        const int c = tid + i * NT;
-        if (c < L::KCH) {
-          const int key = c / (HD / 8), dc = c % (HD / 8);
-          kst[i] = *reinterpret_cast<const u32x4*>(kg + (size_t)(kt * KT + key) * HD + dc * 8);
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < L::VPT; ++i) {
-        const int c = tid + i * NT;
-        if (c < L::VCH) {
-          const int d = c / (KT / 8), kc = c % (KT / 8);
-          vst[i] = *reinterpret_cast<const u32x4*>(vg + (size_t)d * S + kt * KT + kc * 8);
-        }
-      }
-    };
-    auto sstore = [&](int buf) {
-      char* ks = smem + buf * L::STAGE;
-      char* vs = ks + L::KBYTES;
-#pragma unroll
-      for (int i = 0; i < L::KPT; ++i) {
-        const int c = tid + i * NT;
-        if (c < L::KCH) {
-          const int key = c / (HD / 8), dc = c % (HD / 8);
-          *reinterpret_cast<u32x4*>(ks + key * L::KROW + dc * 16) = kst[i];
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < L::VPT; ++i) {
-        const int c = tid + i * NT;
-        if (c < L::VCH) {
-          const int d = c / (KT / 8), kc = c % (KT / 8);
-          *reinterpret_cast<u32x4*>(vs + d * L::VROW + kc * 16) = vst[i];
-        }
-      }
-    };
-
-    __syncthreads();  // previous pass finished reading the LDS stages
-    gload(0);
-    sstore(0);
-    __syncthreads();
-
-    for (int kt = 0; kt < nkt; ++kt) {
-      if (kt + 1 < nkt) gload(kt + 1);
-      const char* ks = smem + (kt & 1) * L::STAGE;
-      const char* vs = ks + L::KBYTES;
-
-      // S^T (64 keys x 32 tokens) = K Q^T
-      f32x16 sacc[2] = {f32x16{}, f32x16{}};
+    // S^T (64 keys x 32 tokens) = K Q^T for the tile in K slot `slot`
+    auto qk = [&](int slot, f32x16 (&sacc)[2]) {
+      const char* ks = kring + slot * L::KBYTES;
+      sacc[0] = f32x16{};
+      sacc[1] = f32x16{};
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
         const u32x4 a0 = *reinterpret_cast<const u32x4*>(ks + col * L::KROW + (16 * s + 8 * half) * 2);
-        const u32x4 a1 =
-            *reinterpret_cast<const u32x4*>(ks + (32 + col) * L::KROW + (16 * s + 8 * half) * 2);
+        const u32x4 a1 = *reinterpret_cast<const u32x4*>(ks + (32 + col) * L::KROW + (16 * s + 8 * half) * 2);
         sacc[0] = mfma_bf16_32x32x16(a0, qreg[s], sacc[0]);
         sacc[1] = mfma_bf16_32x32x16(a1, qreg[s], sacc[1]);
       }
+    };
+    // causal mask (diagonal tile only), row max, threshold rescale of O / l
+    auto rowmax_rescale = [&](int kt, f32x16 (&sacc)[2]) {
       const int k0 = kt * KT;
-      if (k0 + KT - 1 > t0) {  // tile crosses the diagonal: mask keys after the query
+      if (k0 + KT - 1 > t0) {
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
@@ -221,59 +230,77 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[1][r]);
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float mnew = fmaxf(m, mx);
-      // rescale only when some row max of this wave grew (alpha == 1 exactly otherwise)
-      if (__any(mnew > m)) {
+      if (__any(mx > m + RESCALE_T)) {
+        const float mnew = fmaxf(m, mx);
         const float alpha = fast_exp2(m - mnew);
         l *= alpha;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+        m = mnew;
       }
-      m = mnew;
-
-      u32x4 pb[2][2];
+    };
+    // P = exp2(S - m) rounded to bf16 (row sum from that bf16 P), O^T += V^T P^T for V slot `vslot`
+    auto softmax_pv = [&](int vslot, const f32x16 (&sacc)[2]) {
+      const char* vs = vring + vslot * L::VBYTES;
       float psum = 0.f;
 #pragma unroll
       for (int c = 0; c < 2; ++c)
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
-          u32x4 v;
+          u32x4 pb;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const float p0 = fast_exp2(sacc[c][8 * s2 + 2 * e] - mnew);
-            const float p1 = fast_exp2(sacc[c][8 * s2 + 2 * e + 1] - mnew);
-            const uint32_t pk = pack_bf2(p0, p1);
-            psum = dot2_bf16_sum(pk, psum);   // row sum of exactly the bf16 P used for PV
-            v[e] = pk;
+            const float p0 = fast_exp2(sacc[c][8 * s2 + 2 * e] - m);
+            const float p1 = fast_exp2(sacc[c][8 * s2 + 2 * e + 1] - m);
+            pb[e] = pack_bf2(p0, p1);
+            psum = dot2_bf16_sum(pb[e], psum);
           }
-          pb[c][s2] = v;
-        }
-      l += psum;
-
-      // O^T (hd x 32 tokens) += V^T P^T
-#pragma unroll
-      for (int c = 0; c < 2; ++c)
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
           const int key0 = 32 * c + 16 * s2 + 4 * half;
 #pragma unroll
           for (int dt = 0; dt < DT; ++dt) {
             const char* vrow = vs + (dt * 32 + col) * L::VROW;
             const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow + key0 * 2);
             const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + (key0 + 8) * 2);
-            const u32x4 a = {lo[0], lo[1], hi[0], hi[1]};
-            o[dt] = mfma_bf16_32x32x16(a, pb[c][s2], o[dt]);
+            o[dt] = mfma_bf16_32x32x16(u32x4{lo[0], lo[1], hi[0], hi[1]}, pb, o[dt]);
           }
         }
+      l += psum;
+    };
 
-      if (kt + 1 < nkt) sstore((kt + 1) & 1);
-      __syncthreads();
+    // ---- prologue: K(0), V(0), K(1) staged; S(0) computed
+    __syncthreads();   // the previous pass (output staging) is done with the LDS
+    gload_k(0);
+    gload_v(0);
+    sstore_k(0);
+    sstore_v(0);
+    if (nkt > 1) {
+      gload_k(1);
+      sstore_k(1);
     }
+    __syncthreads();
+    f32x16 scur[2], snext[2];
+    qk(0, scur);
+    rowmax_rescale(0, scur);
+
+    // ---- steady state: iteration t issues QK(t+1), softmax + PV(t), and stages K(t+2), V(t+1)
+    for (int t = 0; t + 1 < nkt; ++t) {
+      gload_k(min(t + 2, nkt - 1));   // the clamped reload at the end lands in a free slot
+      gload_v(t + 1);
+      qk((t + 1) % L::NK, snext);
+      softmax_pv(t % L::NV, scur);
+      sstore_k((t + 2) % L::NK);
+      sstore_v((t + 1) % L::NV);
+      __syncthreads();
+      rowmax_rescale(t + 1, snext);
+      scur[0] = snext[0];
+      scur[1] = snext[1];
+    }
+    softmax_pv((nkt - 1) % L::NV, scur);
+    __syncthreads();   // every wave is done with the rings before the output staging reuses them
 
     l += __shfl_xor(l, 32, 64);
     const float inv = 1.f / l;
-    // stage this wave's (32 tokens x hd) output tile in LDS (the K/V stages are free after the last
-    // barrier of the loop), then write whole rows with 16-byte stores
+    // stage this wave's (32 tokens x hd) output tile in LDS, then write whole rows with 16-byte stores
     constexpr int OROW = HD * 2 + 16;
     char* ot = smem + w * (QT * OROW);
 #pragma unroll
@@ -316,7 +343,6 @@ int launch_attn_hd(const AttnArgs& a, hipStream_t st, int stages) {
   }
   return MK_OK;
 }
-
 
 // ---- last-token attention (mk_jax.py:492-520): one query per sequence against all S keys.
 // Kernel 1: workgroup = (256-key chunk, kv head, sequence); thread = key.  Writes per (head,
