@@ -14,6 +14,9 @@
 //                  mk_mlp.py:95-96     out = bf16(x + acc * (s_h * s_d))   (int8 W_down)
 //   linear         mk_jax.py:243,265   bf16(acc) / bf16((acc * s_x) * s_w), then bf16 residual
 //                                      add x + o (mk_jax.py:394)
+#include <cmath>
+#include <cstdlib>
+
 #include "kernels.h"
 #include "mk_common.h"
 
@@ -21,10 +24,33 @@ namespace mk {
 
 namespace {
 
-constexpr int BM = 256, BN = 128;
-constexpr int BKB = 64;             // K bytes per LDS stage
-constexpr int NST = 3;              // LDS ring stages (two in flight while one is consumed)
-constexpr int GT = 256;             // threads per workgroup (2 x 2 waves, 128 x 64 per wave)
+constexpr int BKB = 64;   // K bytes per LDS stage (two MFMA k-steps)
+
+// Block tile BM x BN computed by WGM x WGN waves, NST-stage LDS ring.
+template <int BM_, int BN_, int WGM_, int WGN_, int NST_, int OCC_, int LOOP_ = 0>
+struct GemmCfg {
+  static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_, NST = NST_, OCC = OCC_;
+  // main loop: 0 split k-step pipeline, 1 ping-pong (two wave groups)
+  static constexpr int LOOP = LOOP_;
+  static constexpr int NW = WGM * WGN, NTH = 64 * NW;
+  static constexpr int WM = BM / WGM, WN = BN / WGN;     // wave tile
+  static constexpr int MT = WM / 32, NTL = WN / 32;       // 32x32 MFMA tiles per wave
+  static constexpr int A_BYTES = BM * BKB, ST_BYTES = (BM + BN) * BKB;
+  static constexpr int AQ = BM / 16 / NW, BQ = BN / 16 / NW;   // 1 KB async-load instructions per wave
+  static constexpr int EROW = WN * 4 + 16;                // epilogue LDS row (f32 + pad)
+  static_assert(BM % (16 * NW) == 0 && BN % (16 * NW) == 0, "load split");
+  static_assert(NW * 32 * EROW <= NST * ST_BYTES, "epilogue staging fits in the ring");
+  static_assert(WN % 64 == 0 || WN == 32, "wave tile width");
+  static_assert(LOOP != 1 || (WGM == 2 && NST >= 3), "ping-pong needs two wave groups and two stages in flight");
+};
+// 256x256 block, 128x128 per wave (accumulators in AGPRs), one workgroup per CU
+using CfgL = GemmCfg<256, 256, 2, 2, 3, 1, 0>;
+// 256x128 block, 128x64 per wave, two workgroups per CU
+using CfgM = GemmCfg<256, 128, 2, 2, 3, 2>;
+// 128x128 block, 64x64 per wave, three workgroups per CU
+using CfgS = GemmCfg<128, 128, 2, 2, 3, 3>;
+// 256x256 block, 8 waves of 128x64 (two per SIMD), one workgroup per CU
+using CfgX = GemmCfg<256, 256, 2, 4, 4, 1, 1>;
 
 template <GemmIn IN>
 struct Mma;
@@ -52,8 +78,7 @@ __device__ inline float silu_mul(float g, float u) {
   return g / (1.f + __expf(-g)) * u;
 }
 
-// Applies the epilogue to one accumulator element at (m, n).  For DQ_SILU* the pair (g, u) comes
-// from two tiles; `v` is g and `u` the matching up value, `nh` the logical intermediate column.
+// One accumulator element of the skinny kernel at (m, n) through the epilogue.
 template <Epi EPI>
 __device__ inline void epi_store(const GemmArgs& g, int m, int n, float v) {
   if constexpr (EPI == Epi::DQ_BF16) {
@@ -86,207 +111,321 @@ __device__ inline int swz(int row) { return (row >> 2) & 3; }
 
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
+// 16-byte global -> LDS copy that bypasses VGPRs (global_load_lds_dwordx4).  Kept in a non-template
+// function: in a template kernel with dependent arguments the host pass of clang rejects the builtin
+// silently and then emits no launch stub for the kernel.
+__device__ inline void copy16_to_lds(const char* src, char* dst) {
+  __builtin_amdgcn_global_load_lds(src, (lds_ptr)dst, 16, 0, 0);
+}
+
+// Workgroup barrier for the LDS ring.  A bare s_barrier: __syncthreads() adds a fence that would also
+// drain the younger stages' async loads.  The empty asm statements keep the compiler from moving LDS
+// accesses across it.
+__device__ inline void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // s_waitcnt with only the vector-memory counter constrained (gfx9 encoding: vmcnt[3:0], expcnt[6:4],
 // lgkmcnt[11:8], vmcnt[5:4] in [15:14]).
 #define MK_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14))
 
-template <GemmIn IN, Epi EPI>
-__global__ __launch_bounds__(GT, 2) void gemm_kernel(GemmArgs g) {
+template <int BM, int BN, int WGM, int WGN, int NST, int OCC, int LOOP, GemmIn IN, Epi EPI>
+__global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
+  using C = GemmCfg<BM, BN, WGM, WGN, NST, OCC, LOOP>;
   using T = Mma<IN>;
   using Acc = typename T::Acc;
-  constexpr int A_BYTES = BM * BKB, ST_BYTES = (BM + BN) * BKB;
-  __shared__ __attribute__((aligned(1024))) char smem[NST * ST_BYTES];
+  __shared__ __attribute__((aligned(1024))) char smem[C::NST * C::ST_BYTES];
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index, kept in an SGPR
   const int col = lane & 31, half = lane >> 5;
-  const int wm = w >> 1, wn = w & 1;
-  // XCD-aware tile order: consecutive tiles (same A rows, neighbouring B columns) share an XCD's L2
-  const int ntn = gridDim.x, nblk = gridDim.x * gridDim.y;
+  const int wm = w / C::WGN, wn = w % C::WGN;
+  // Tile order.  Workgroups are dispatched round-robin over the 8 XCDs, each with its own L2: launch id
+  // lid runs on XCD lid % 8, so XCD x is given the contiguous work range [x, x + 1) * nblk / 8.  Work
+  // ids walk GM-row groups column by column, so the ~32-64 tiles an XCD runs at once form a compact
+  // block that reuses both A row panels and B column panels from its L2.
+  const int ntn = gridDim.x, ntm = gridDim.y, nblk = gridDim.x * gridDim.y;
   const int lid = blockIdx.x + ntn * blockIdx.y;
   const int work = (nblk % 8 == 0) ? (lid % 8) * (nblk / 8) + lid / 8 : lid;
-  const int m0 = (work / ntn) * BM, n0 = (work % ntn) * BN;
+  constexpr int GM = 8;
+  const int grp = work / (GM * ntn), first_m = grp * GM, gsz = min(ntm - first_m, GM);
+  const int wig = work - grp * GM * ntn;
+  const int m0 = (first_m + wig % gsz) * C::BM, n0 = (wig / gsz) * C::BN;
   const int lda = g.lda * T::ESZ, ldb = g.ldb * T::ESZ;   // bytes
   const int Kb = g.K * T::ESZ;
+  constexpr int Q = C::AQ + C::BQ;                        // async-load instructions per wave per stage
 
-  // this lane's async-load sources: A rows 16 q + lane / 4 (q = 4 w + j), B rows 16 q + lane / 4
-  // (q = 2 w + j); rows past M / N are clamped (their results are never stored)
-  const char* asrc[4];
-  const char* bsrc[2];
+  // this lane's async-load sources: rows 16 q + lane / 4 of A (q = AQ w + j) and B (q = BQ w + j) as
+  // 32-bit byte offsets from the operand base (the base and the K offset stay scalar); rows past M / N
+  // are clamped (their results are never stored)
+  uint32_t aoff[C::AQ], boff[C::BQ];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int r = 16 * (4 * w + j) + (lane >> 2);
-    const int gr = min(m0 + r, g.M - 1);
-    asrc[j] = static_cast<const char*>(g.A) + (size_t)gr * lda + 16 * ((lane & 3) ^ swz(r));
+  for (int j = 0; j < C::AQ; ++j) {
+    const int r = 16 * (C::AQ * w + j) + (lane >> 2);
+    aoff[j] = (uint32_t)min(m0 + r, g.M - 1) * (uint32_t)lda + 16u * ((lane & 3) ^ swz(r));
   }
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int r = 16 * (2 * w + j) + (lane >> 2);
-    const int gr = min(n0 + r, g.N - 1);
-    bsrc[j] = static_cast<const char*>(g.B) + (size_t)gr * ldb + 16 * ((lane & 3) ^ swz(r));
+  for (int j = 0; j < C::BQ; ++j) {
+    const int r = 16 * (C::BQ * w + j) + (lane >> 2);
+    boff[j] = (uint32_t)min(n0 + r, g.N - 1) * (uint32_t)ldb + 16u * ((lane & 3) ^ swz(r));
   }
-  auto issue = [&](int st, int kb) {
-    char* base = smem + st * ST_BYTES;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      __builtin_amdgcn_global_load_lds(asrc[j] + kb, (lds_ptr)(base + (4 * w + j) * 1024), 16, 0, 0);
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-      __builtin_amdgcn_global_load_lds(bsrc[j] + kb, (lds_ptr)(base + A_BYTES + (2 * w + j) * 1024), 16, 0, 0);
+  const char* const Ag = static_cast<const char*>(g.A);
+  const char* const Bg = static_cast<const char*>(g.B);
+  // async load j (of Q) of stage `st` at K byte offset kb
+  auto issue1 = [&](int j, int st, int kb) {
+    char* base = smem + st * C::ST_BYTES;
+    if (j < C::AQ) copy16_to_lds(Ag + kb + aoff[j], base + (C::AQ * w + j) * 1024);
+    else copy16_to_lds(Bg + kb + boff[j - C::AQ], base + C::A_BYTES + (C::BQ * w + j - C::AQ) * 1024);
   };
 
-  Acc acc[4][2];
+  Acc acc[C::MT][C::NTL];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < C::MT; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = Acc{};
+    for (int j = 0; j < C::NTL; ++j) acc[i][j] = Acc{};
 
-  int arow[4], brow[2];
+  // LDS operand reads.  Row wm WM + 32 mt + col of A has swizzle swz(col) (WM and 32 are multiples of
+  // 16), so tile mt is a fixed 2 KB step from tile 0 and the per-k-step lane offsets are two registers.
+  const int sw = swz(col);
+  const int aro = (wm * C::WM + col) * BKB, bro = C::A_BYTES + (wn * C::WN + col) * BKB;
+  const int ao0 = aro + 16 * (half ^ sw), ao1 = aro + 16 * ((2 + half) ^ sw);
+  const int bo0 = bro + 16 * (half ^ sw), bo1 = bro + 16 * ((2 + half) ^ sw);
+  auto rd = [&](const char* S, int ao, int bo, u32x4 (&ra)[C::MT], u32x4 (&rb)[C::NTL]) {
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt) arow[mt] = wm * 128 + mt * 32 + col;
+    for (int nt = 0; nt < C::NTL; ++nt) rb[nt] = *reinterpret_cast<const u32x4*>(S + bo + nt * 32 * BKB);
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) brow[nt] = wn * 64 + nt * 32 + col;
+    for (int mt = 0; mt < C::MT; ++mt) ra[mt] = *reinterpret_cast<const u32x4*>(S + ao + mt * 32 * BKB);
+  };
+  constexpr int NMF = C::MT * C::NTL;
+  auto mf = [&](int i, const u32x4 (&ra)[C::MT], const u32x4 (&rb)[C::NTL]) {
+    const int mt = i / C::NTL, nt = i % C::NTL;
+    acc[mt][nt] = T::run(ra[mt], rb[nt], acc[mt][nt]);
+  };
+
+  // Software pipeline over the LDS ring (stage = BKB bytes of K = two MFMA k-steps):
+  //   R0 / R1 hold the operands of k-step 0 / 1.  Iteration it: read k-step 1 of stage it into R1;
+  //   the MFMAs of k-step 0 interleaved with the async loads of stage it + NST - 1; part of k-step 1's
+  //   MFMAs; wait for stage it + 1, barrier, read its k-step 0 into R0; the rest of k-step 1's MFMAs.
+  //   The MFMA pipe always has queued work while LDS reads and the barrier are in flight.
+  // sched_barrier(0) keeps the compiler's scheduler from merging the phases.
+  // Epilogue inputs that do not depend on the accumulators (row and column scales), loaded before the
+  // main loop so that their latency is hidden.  Epilogue task i of a lane covers row trow0 + i * TRS of
+  // a 32-row slice and a fixed group of 8 columns (8 gate + 8 up columns for the SiLU epilogues).
+  constexpr bool SILU = EPI == Epi::DQ_SILU || EPI == Epi::DQ_SILU_F32A || EPI == Epi::SILU_BF16;
+  constexpr bool RES = EPI == Epi::RES_BF16ADD || EPI == Epi::DQ_RES_BF16ADD || EPI == Epi::RES_F32ADD ||
+                       EPI == Epi::DQ2_RES_F32ADD;
+  constexpr bool DQ = EPI == Epi::DQ_BF16 || EPI == Epi::DQ2_BF16 || EPI == Epi::DQ_RES_BF16ADD ||
+                      EPI == Epi::DQ2_RES_F32ADD || EPI == Epi::DQ_SILU || EPI == Epi::DQ_SILU_F32A ||
+                      EPI == Epi::SILU_BF16;    // SILU_BF16: only when scales are given
+  constexpr int TPR = SILU ? C::WN / 16 : C::WN / 8;   // tasks per row
+  constexpr int TRS = 64 / TPR;                        // rows between a lane's tasks
+  constexpr int NTASK = 32 / TRS;
+  static_assert(64 % TPR == 0 && 32 % TRS == 0, "epilogue task split");
+  static_assert(!SILU || C::WN % 64 == 0, "SiLU epilogue needs whole [gate | up] column blocks per wave");
+  const int tcol = lane % TPR, trow0 = lane / TPR;
+  const int nb0 = n0 + wn * C::WN;                     // first column of the wave
+  // SiLU: 64-column block blk of the wave is [32 gate | 32 up]; this lane's gate columns start at pg
+  const int pg = SILU ? min(nb0 + (tcol >> 2) * 64, g.N - 64) + (tcol & 3) * 8 : 0;
+  const int pc = SILU ? pg : min(nb0 + tcol * 8, g.N - 8);
+  const bool dq = DQ && g.rs != nullptr;
+  float rsv[C::MT][NTASK];
+  f32x4 csv[SILU ? 4 : 2];
+  if (dq) {
+#pragma unroll
+    for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < NTASK; ++i) rsv[mt][i] = g.rs[min(m0 + wm * C::WM + mt * 32 + trow0 + i * TRS, g.M - 1)];
+    csv[0] = *reinterpret_cast<const f32x4*>(g.cs + pc);
+    csv[1] = *reinterpret_cast<const f32x4*>(g.cs + pc + 4);
+    if constexpr (SILU) {
+      csv[2] = *reinterpret_cast<const f32x4*>(g.cs + pc + 32);
+      csv[3] = *reinterpret_cast<const f32x4*>(g.cs + pc + 36);
+    }
+  }
 
   const int nk = Kb / BKB;
-  issue(0, 0);
-  if (nk > 1) issue(1, BKB);
-  for (int it = 0; it < nk; ++it) {
-    if (it + 1 < nk) MK_WAIT_VMCNT(6);   // this stage's 6 loads done; the next stage's may be in flight
-    else MK_WAIT_VMCNT(0);
-    // every wave's part of the stage is in LDS and every wave is done with stage it-1.  A bare
-    // s_barrier: __syncthreads() adds a fence that would also drain the next stage's loads.
-    __builtin_amdgcn_s_barrier();
-    if (it + 2 < nk) issue((it + 2) % NST, (it + 2) * BKB);
-    const char* As = smem + (it % NST) * ST_BYTES;
-    const char* Bs = As + A_BYTES;
 #pragma unroll
-    for (int ks = 0; ks < BKB / 32; ++ks) {
-      const int c = 2 * ks + half;
-      u32x4 bop[2];
+  for (int s0 = 0; s0 < C::NST - 1; ++s0)
+    if (s0 < nk) {
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt)
-        bop[nt] = *reinterpret_cast<const u32x4*>(Bs + brow[nt] * BKB + 16 * (c ^ swz(brow[nt])));
+      for (int j = 0; j < Q; ++j) issue1(j, s0, s0 * BKB);
+    }
+  if (nk >= C::NST - 1) MK_WAIT_VMCNT((C::NST - 2) * Q);
+  else MK_WAIT_VMCNT(0);
+  lds_barrier();
+  // Materialize the epilogue's kernel arguments now: a scalar load still pending inside the loop would
+  // turn every LDS wait there into lgkmcnt(0) (scalar loads return out of order).
+  asm volatile("" ::"s"(g.out), "s"(g.res), "s"(g.rs), "s"(g.cs), "s"(g.aux), "s"(g.ldo), "s"(g.ldr));
+  u32x4 ra0[C::MT], rb0[C::NTL], ra1[C::MT], rb1[C::NTL];
+  if constexpr (C::LOOP == 1) {
+    // Ping-pong: the waves form two groups (wm = 0, 1) with one wave of each on every SIMD.  Each
+    // iteration is a memory phase M (LDS reads of both k-steps of a stage into registers, async loads
+    // of the stage NST - 1 ahead) and a compute phase C (the stage's MFMAs), each closed by a barrier.
+    // Group 1 starts one barrier late, so on every SIMD one wave issues MFMAs while the other does its
+    // memory phase, and the barrier between phases never drains the MFMA pipe.  Group 0 waits for its
+    // own loads of stage s + 1 at the end of C(s), group 1 at the end of M(s): both before the barrier
+    // after which group 0 reads stage s + 1.  Every wave finishes its LDS reads before the barrier
+    // closing its M phase, so a stage's slot is refilled only after both groups have read it.
+    constexpr int D = C::NST - 1;
+    if (wm == 1) lds_barrier();
+    int cur = 0;
+    for (int it = 0; it < nk; ++it) {
+      const char* S = smem + cur * C::ST_BYTES;
+      rd(S, ao0, bo0, ra0, rb0);
+      rd(S, ao1, bo1, ra1, rb1);
+      const bool pre = it + D < nk;
+      if (pre) {
+        const int nslot = cur == 0 ? C::NST - 1 : cur - 1;
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
-        const u32x4 aop = *reinterpret_cast<const u32x4*>(As + arow[mt] * BKB + 16 * (c ^ swz(arow[mt])));
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = T::run(aop, bop[nt], acc[mt][nt]);
+        for (int j = 0; j < Q; ++j) issue1(j, nslot, (it + D) * BKB);
       }
+      __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's reads of the stage are done
+      if (wm == 1) {
+        if (pre) MK_WAIT_VMCNT((D - 1) * Q);
+        else MK_WAIT_VMCNT(0);
+      }
+      lds_barrier();
+      __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+      for (int i = 0; i < NMF; ++i) mf(i, ra0, rb0);
+#pragma unroll
+      for (int i = 0; i < NMF; ++i) mf(i, ra1, rb1);
+      __builtin_amdgcn_s_setprio(0);
+      if (wm == 0) {
+        if (pre) MK_WAIT_VMCNT((D - 1) * Q);
+        else MK_WAIT_VMCNT(0);
+      }
+      lds_barrier();
+      cur = cur == C::NST - 1 ? 0 : cur + 1;
+    }
+    if (wm == 0) lds_barrier();
+  } else {
+    rd(smem, ao0, bo0, ra0, rb0);
+    int cur = 0;                                            // stage slot of iteration it
+    constexpr int SPLIT = NMF / 4;                          // k-step 1 MFMAs issued before the barrier
+    for (int it = 0; it < nk; ++it) {
+      const char* S = smem + cur * C::ST_BYTES;
+      // R0's reads (issued a dozen MFMAs ago) are done; waiting for them here keeps the outstanding LDS
+      // reads within what lgkmcnt can count, so the k-step 1 reads below overlap the k-step 0 MFMAs
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+      rd(S, ao1, bo1, ra1, rb1);
+      __builtin_amdgcn_sched_barrier(0);
+      const bool pre = it + C::NST - 1 < nk;
+      const int nslot = cur == 0 ? C::NST - 1 : cur - 1;    // slot of stage it + NST - 1 (= it - 1)
+      const int nkb = (it + C::NST - 1) * BKB;
+#pragma unroll
+      for (int i = 0; i < NMF; ++i) {
+        mf(i, ra0, rb0);
+        if (i < Q && pre) issue1(i, nslot, nkb);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (Q > NMF && pre) {
+#pragma unroll
+        for (int j = NMF; j < Q; ++j) issue1(j, nslot, nkb);
+      }
+#pragma unroll
+      for (int i = 0; i < SPLIT; ++i) mf(i, ra1, rb1);
+      __builtin_amdgcn_sched_barrier(0);
+      cur = cur == C::NST - 1 ? 0 : cur + 1;
+      if (it + 1 < nk) {
+        // stage it + 1 landed for this wave, then for every wave; every wave finished reading stage it
+        if (pre) MK_WAIT_VMCNT((C::NST - 2) * Q);
+        else MK_WAIT_VMCNT(0);
+        lds_barrier();
+        rd(smem + cur * C::ST_BYTES, ao0, bo0, ra0, rb0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = SPLIT; i < NMF; ++i) mf(i, ra1, rb1);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 
   // ---- epilogue through LDS.  The accumulators of a 32x32 tile sit column-wise across lanes (lane:
-  // column, 16 rows); each half (64 rows x 64 cols) of the wave's tile is written to the wave's own
-  // LDS region, then every lane handles 8 consecutive columns of a row with 16-byte accesses, all
-  // loads of a batch issued before its stores.
-  __builtin_amdgcn_s_barrier();   // every wave is done reading the LDS ring
-  constexpr int EROW = 64 * 4 + 16;
-  char* er = smem + w * 64 * EROW;
+  // column, 16 rows); each 32-row slice of the wave's tile is written to the wave's own LDS region,
+  // then every lane handles 8 consecutive columns of a row with 16-byte accesses.  The residual rows of
+  // slice mt + 1 are loaded while slice mt is processed.
+  u32x4 rv[2][NTASK];
+  auto load_res = [&](int mt, u32x4 (&dst)[NTASK]) {
 #pragma unroll
-  for (int hh = 0; hh < 2; ++hh) {
+    for (int i = 0; i < NTASK; ++i) {
+      const int m = min(m0 + wm * C::WM + mt * 32 + trow0 + i * TRS, g.M - 1);
+      dst[i] = *reinterpret_cast<const u32x4*>(g.res + (size_t)m * g.ldr + pc);
+    }
+  };
+  if constexpr (RES) load_res(0, rv[0]);
+  lds_barrier();   // every wave is done reading the LDS ring
+  constexpr int EROW = C::EROW;
+  char* er = smem + w * 32 * EROW;
+  using V4 = typename T::Vec4;
 #pragma unroll
-    for (int m2 = 0; m2 < 2; ++m2)
+  for (int mt = 0; mt < C::MT; ++mt) {
+    if constexpr (RES) {
+      if (mt + 1 < C::MT) load_res(mt + 1, rv[(mt + 1) & 1]);
+    }
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt)
+    for (int nt = 0; nt < C::NTL; ++nt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int lr = m2 * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-          *reinterpret_cast<typename T::Elem*>(er + lr * EROW + (nt * 32 + col) * 4) = acc[2 * hh + m2][nt][r];
-        }
+      for (int r = 0; r < 16; ++r) {
+        const int lr = 8 * (r >> 2) + 4 * half + (r & 3);
+        *reinterpret_cast<typename T::Elem*>(er + lr * EROW + (nt * 32 + col) * 4) = acc[mt][nt][r];
+      }
     __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's LDS writes are done
     __builtin_amdgcn_wave_barrier();
-    const int mrow0 = m0 + wm * 128 + hh * 64;
-    if constexpr (EPI == Epi::DQ_SILU || EPI == Epi::DQ_SILU_F32A || EPI == Epi::SILU_BF16) {
-      // 32 gate columns then 32 up columns: 64 rows x 32 h columns = 256 tasks of 8 columns
-      const int p0 = n0 + wn * 64;
-      const int nh0 = p0 / 2;
-      const bool dq = g.rs != nullptr;
-      float vg[4][8], vu[4][8], rsv[4];
-      f32x4 sgc[4][2], suc[4][2];
+    const int mrow0 = m0 + wm * C::WM + mt * 32;
+    if constexpr (SILU) {
+      const int blk = tcol >> 2, j0 = (tcol & 3) * 8;
+      const int p0 = nb0 + blk * 64, nh = p0 / 2 + j0;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int t = lane + 64 * i, lr = t >> 2, j0 = (t & 3) * 8;
-        using V4 = typename T::Vec4;
-        const V4* gp = reinterpret_cast<const V4*>(er + lr * EROW + j0 * 4);
-        const V4* up = reinterpret_cast<const V4*>(er + lr * EROW + (32 + j0) * 4);
+      for (int i = 0; i < NTASK; ++i) {
+        const int lr = trow0 + i * TRS, m = mrow0 + lr;
+        const V4* gp = reinterpret_cast<const V4*>(er + lr * EROW + (blk * 64 + j0) * 4);
+        const V4* up = reinterpret_cast<const V4*>(er + lr * EROW + (blk * 64 + 32 + j0) * 4);
         const V4 g0 = gp[0], g1 = gp[1], u0 = up[0], u1 = up[1];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          vg[i][e] = T::f(g0[e]);
-          vg[i][4 + e] = T::f(g1[e]);
-          vu[i][e] = T::f(u0[e]);
-          vu[i][4 + e] = T::f(u1[e]);
-        }
-        const int m = min(mrow0 + lr, g.M - 1);
-        rsv[i] = dq ? g.rs[m] : 1.f;
-        if (dq) {
-          sgc[i][0] = *reinterpret_cast<const f32x4*>(g.cs + p0 + j0);
-          sgc[i][1] = *reinterpret_cast<const f32x4*>(g.cs + p0 + j0 + 4);
-          suc[i][0] = *reinterpret_cast<const f32x4*>(g.cs + p0 + 32 + j0);
-          suc[i][1] = *reinterpret_cast<const f32x4*>(g.cs + p0 + 32 + j0 + 4);
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int t = lane + 64 * i, lr = t >> 2, j0 = (t & 3) * 8;
-        const int m = mrow0 + lr;
         if (m >= g.M || p0 >= g.N) continue;
         float h[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float sg = dq ? (e < 4 ? sgc[i][0][e] : sgc[i][1][e - 4]) : 1.f;
-          const float su = dq ? (e < 4 ? suc[i][0][e] : suc[i][1][e - 4]) : 1.f;
+          const float gacc = T::f(e < 4 ? g0[e] : g1[e - 4]);
+          const float uacc = T::f(e < 4 ? u0[e] : u1[e - 4]);
+          const float sg = dq ? csv[e >> 2][e & 3] : 1.f;
+          const float su = dq ? csv[2 + (e >> 2)][e & 3] : 1.f;
+          const float rs = dq ? rsv[mt][i] : 1.f;
           if constexpr (EPI == Epi::SILU_BF16) {
             // XLA path (mk_jax.py:283-299, :420-421): gu rounded to bf16, silu and product in bf16
-            float gv = vg[i][e], uv = vu[i][e];
+            float gv = gacc, uv = uacc;
             if (dq) {
-              gv = gv * (rsv[i] * sg);
-              uv = uv * (rsv[i] * su);
+              gv = gv * (rs * sg);
+              uv = uv * (rs * su);
             }
             gv = bf2f(f2bf(gv));
             uv = bf2f(f2bf(uv));
             h[e] = bf2f(f2bf(gv / (1.f + __expf(-gv)))) * uv;
           } else {
-            const float gv = (vg[i][e] * rsv[i]) * sg;
-            const float uv = (vu[i][e] * rsv[i]) * su;
-            h[e] = silu_mul(gv, uv);
+            h[e] = silu_mul((gacc * rs) * sg, (uacc * rs) * su);
           }
         }
         if constexpr (EPI == Epi::DQ_SILU_F32A) {
-          float* op = static_cast<float*>(g.out) + (size_t)m * g.ldo + nh0 + j0;
-          const f32x4 a0 = *reinterpret_cast<const f32x4*>(g.aux + nh0 + j0);
-          const f32x4 a1 = *reinterpret_cast<const f32x4*>(g.aux + nh0 + j0 + 4);
+          float* op = static_cast<float*>(g.out) + (size_t)m * g.ldo + nh;
+          const f32x4 a0 = *reinterpret_cast<const f32x4*>(g.aux + nh);
+          const f32x4 a1 = *reinterpret_cast<const f32x4*>(g.aux + nh + 4);
           reinterpret_cast<f32x4*>(op)[0] = f32x4{h[0] * a0[0], h[1] * a0[1], h[2] * a0[2], h[3] * a0[3]};
           reinterpret_cast<f32x4*>(op)[1] = f32x4{h[4] * a1[0], h[5] * a1[1], h[6] * a1[2], h[7] * a1[3]};
         } else {
-          *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(g.out) + (size_t)m * g.ldo + nh0 + j0) =
+          *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(g.out) + (size_t)m * g.ldo + nh) =
               u32x4{pack_bf2(h[0], h[1]), pack_bf2(h[2], h[3]), pack_bf2(h[4], h[5]), pack_bf2(h[6], h[7])};
         }
       }
     } else {
-      // 64 rows x 64 columns = 512 tasks of 8 columns, 8 per lane
-      constexpr bool RES = EPI == Epi::RES_BF16ADD || EPI == Epi::DQ_RES_BF16ADD || EPI == Epi::RES_F32ADD ||
-                           EPI == Epi::DQ2_RES_F32ADD;
-      constexpr bool DQ = EPI == Epi::DQ_BF16 || EPI == Epi::DQ2_BF16 || EPI == Epi::DQ_RES_BF16ADD ||
-                          EPI == Epi::DQ2_RES_F32ADD;
-      const int nb0 = n0 + wn * 64;
-      u32x4 rv[8];
-      float rsv[8];
+      const int c8 = tcol * 8, n = nb0 + c8;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int t = lane + 64 * i, lr = t >> 3, c8 = (t & 7) * 8;
-        const int m = min(mrow0 + lr, g.M - 1);
-        const int n = min(nb0 + c8, g.N - 8);
-        if constexpr (RES) rv[i] = *reinterpret_cast<const u32x4*>(g.res + (size_t)m * g.ldr + n);
-        if constexpr (DQ) rsv[i] = g.rs[m];
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int t = lane + 64 * i, lr = t >> 3, c8 = (t & 7) * 8;
-        const int m = mrow0 + lr, n = nb0 + c8;
-        if (m >= g.M || n >= g.N) continue;
-        using V4 = typename T::Vec4;
+      for (int i = 0; i < NTASK; ++i) {
+        const int lr = trow0 + i * TRS, m = mrow0 + lr;
         const V4* vp = reinterpret_cast<const V4*>(er + lr * EROW + c8 * 4);
         const V4 r0 = vp[0], r1 = vp[1];
+        if (m >= g.M || n >= g.N) continue;
         if constexpr (EPI == Epi::I32) {
           V4* op = reinterpret_cast<V4*>(static_cast<int32_t*>(g.out) + (size_t)m * g.ldo + n);
           op[0] = r0;
@@ -306,13 +445,11 @@ __global__ __launch_bounds__(GT, 2) void gemm_kernel(GemmArgs g) {
           continue;
         }
         if constexpr (DQ) {
-          const f32x4 c0 = *reinterpret_cast<const f32x4*>(g.cs + n);
-          const f32x4 c1 = *reinterpret_cast<const f32x4*>(g.cs + n + 4);
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
-            const float cs = e < 4 ? c0[e] : c1[e - 4];
-            if constexpr (EPI == Epi::DQ2_BF16 || EPI == Epi::DQ2_RES_F32ADD) v[e] = v[e] * (rsv[i] * cs);
-            else v[e] = (v[e] * rsv[i]) * cs;
+            const float cs = csv[e >> 2][e & 3];
+            if constexpr (EPI == Epi::DQ2_BF16 || EPI == Epi::DQ2_RES_F32ADD) v[e] = v[e] * (rsv[mt][i] * cs);
+            else v[e] = (v[e] * rsv[mt][i]) * cs;
           }
         }
         u32x4 o;
@@ -320,7 +457,7 @@ __global__ __launch_bounds__(GT, 2) void gemm_kernel(GemmArgs g) {
         for (int e = 0; e < 4; ++e) {
           float a = v[2 * e], b = v[2 * e + 1];
           if constexpr (RES) {
-            const float ra = bf_lo(rv[i][e]), rb = bf_hi(rv[i][e]);
+            const float ra = bf_lo(rv[mt & 1][i][e]), rb = bf_hi(rv[mt & 1][i][e]);
             if constexpr (EPI == Epi::RES_BF16ADD || EPI == Epi::DQ_RES_BF16ADD) {
               a = ra + bf2f(f2bf(a));
               b = rb + bf2f(f2bf(b));
@@ -384,10 +521,51 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_kernel(GemmArgs g) 
   }
 }
 
+// Tile configuration for a problem.  The busiest CU runs ceil(tiles / 256) tiles (the order spreads
+// them evenly), so the estimate is ceil(tiles / 256) * tile area / relative throughput, the throughputs
+// measured on MI355X at the model's shapes (random data): the 8-wave ping-pong 256x256 tile is fastest
+// per tile, except for the SiLU epilogue, whose VALU work is hidden better by two co-resident
+// 256x128 workgroups.
+int choose_cfg(const GemmArgs& g) {
+  if (g.cfg >= 1 && g.cfg <= 4) return g.cfg;
+  static const int forced = [] {
+    const char* e = std::getenv("MK_GEMM_CFG");   // tuning override: 1 | 2 | 3 | 4
+    return e ? std::atoi(e) : 0;
+  }();
+  if (forced >= 1 && forced <= 4) return forced;
+  const bool silu = g.epi == Epi::DQ_SILU || g.epi == Epi::DQ_SILU_F32A || g.epi == Epi::SILU_BF16;
+  struct Opt { int id, bm, bn; double eff; };
+  const Opt opts[4] = {{4, 256, 256, silu ? 1.05 : 1.25}, {2, 256, 128, 1.0}, {1, 256, 256, 0.9},
+                       {3, 128, 128, 0.85}};
+  int best = 2;
+  double bt = 1e300;
+  for (const Opt& o : opts) {
+    if (silu && o.id == 3) continue;                 // 64-column waves: fine, but never faster
+    const double tiles = (double)((g.M + o.bm - 1) / o.bm) * ((g.N + o.bn - 1) / o.bn);
+    const double t = std::ceil(tiles / 256.0) * o.bm * o.bn / o.eff;
+    if (t < bt * 0.999) {
+      bt = t;
+      best = o.id;
+    }
+  }
+  return best;
+}
+
+template <class C, GemmIn IN, Epi EPI>
+void launch_c(const GemmArgs& g, hipStream_t st) {
+  dim3 grid((g.N + C::BN - 1) / C::BN, (g.M + C::BM - 1) / C::BM);
+  hipLaunchKernelGGL((gemm_kernel<C::BM, C::BN, C::WGM, C::WGN, C::NST, C::OCC, C::LOOP, IN, EPI>), grid, dim3(C::NTH),
+                     0, st, g);
+}
+
 template <GemmIn IN, Epi EPI>
 void launch_t(const GemmArgs& g, hipStream_t st) {
-  dim3 grid((g.N + BN - 1) / BN, (g.M + BM - 1) / BM);
-  hipLaunchKernelGGL((gemm_kernel<IN, EPI>), grid, dim3(GT), 0, st, g);
+  switch (choose_cfg(g)) {
+    case 1: launch_c<CfgL, IN, EPI>(g, st); break;
+    case 3: launch_c<CfgS, IN, EPI>(g, st); break;
+    case 4: launch_c<CfgX, IN, EPI>(g, st); break;
+    default: launch_c<CfgM, IN, EPI>(g, st); break;
+  }
 }
 
 template <GemmIn IN, Epi EPI>
@@ -461,6 +639,12 @@ int launch_gemm(const GemmArgs& g, hipStream_t st) {
   if (rc) return rc;
   MK_REQUIRE((g.K * (g.in == GemmIn::I8 ? 1 : 2)) % BKB == 0, "gemm: K bytes must be a multiple of 64");
   MK_REQUIRE(g.N % 8 == 0 && (g.ldo % 8 == 0) && (g.ldr % 8 == 0), "gemm: N and output strides must be multiples of 8");
+  {
+    const uint64_t esz = g.in == GemmIn::I8 ? 1 : 2;
+    MK_REQUIRE((uint64_t)(g.M - 1) * g.lda * esz + g.K * esz < (1ull << 32) &&
+                   (uint64_t)(g.N - 1) * g.ldb * esz + g.K * esz < (1ull << 32),
+               "gemm: each operand must span less than 4 GiB");
+  }
   MK_REQUIRE(((uintptr_t)g.out % 16) == 0 && ((uintptr_t)g.res % 16) == 0 && ((uintptr_t)g.cs % 16) == 0 &&
                  ((uintptr_t)g.aux % 16) == 0,
              "gemm: output, residual and scale vectors must be 16-byte aligned");

@@ -65,6 +65,8 @@ struct GemmArgs {
   const float* rs;            // per-row scale (tokens)
   const float* cs;            // per-column scale (output channels)
   const float* aux;           // DQ_SILU_F32A: per-intermediate-channel factor
+  int cfg;                    // tile configuration: 0 auto, 1 256x256 (4 waves), 2 256x128, 3 128x128,
+                              // 4 256x256 (8 waves)
 };
 int gemm_validate(const GemmArgs& g);
 int launch_gemm(const GemmArgs& g, hipStream_t st);
