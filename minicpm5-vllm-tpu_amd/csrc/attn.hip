@@ -66,8 +66,8 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(const uint16_t* __restri
 template <int HD>
 struct AttnSmem {
   static constexpr int KROW = HD * 2 + 16;   // bytes per K row (padded: conflict-free 16-byte reads)
-  static constexpr int VROW = KT * 2 + 8;    // bytes per V^T row: 136 = 8 (mod 256) -> 8-byte reads of
-                                             // 32 consecutive rows hit distinct banks
+  static constexpr int VROW = KT * 2 + 16;   // bytes per V^T row: 144 = 16 (mod 128) -> 16-byte reads
+                                             // of 8 consecutive rows hit distinct banks
   static constexpr int KBYTES = KT * KROW;
   static constexpr int VBYTES = HD * VROW;
   static constexpr int NK = 3, NV = 2;       // K ring (QK runs one tile ahead), V ring
@@ -152,10 +152,12 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
     for (int i = 0; i < L::VPT; ++i) {
       const int c = tid + i * NT;
       if (L::VCH % NT == 0 || c < L::VCH) {
+        // keys are stored with bits 2 and 3 of their index swapped inside each 16-key group, so the 8
+        // keys a lane's P^T column holds (4 half + {0..3, 8..11}) are 16 contiguous bytes
         const int d = c / (KT / 8), kc = c % (KT / 8);
-        u32x2* dst = reinterpret_cast<u32x2*>(vs + d * L::VROW + kc * 16);   // 8-byte aligned rows
-        dst[0] = u32x2{vst[i][0], vst[i][1]};
-        dst[1] = u32x2{vst[i][2], vst[i][3]};
+        char* row = vs + d * L::VROW + (kc >> 1) * 32 + (kc & 1) * 8;
+        *reinterpret_cast<u32x2*>(row) = u32x2{vst[i][0], vst[i][1]};        // keys 8 kc + 0..3
+        *reinterpret_cast<u32x2*>(row + 16) = u32x2{vst[i][2], vst[i][3]};   // keys 8 kc + 4..7
       }
     }
   };
@@ -255,13 +257,12 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
             pb[e] = pack_bf2(p0, p1);
             psum = dot2_bf16_sum(pb[e], psum);
           }
-          const int key0 = 32 * c + 16 * s2 + 4 * half;
+          // keys 32 c + 16 s2 + 4 half + {0..3, 8..11}: stored contiguously (see sstore_v)
+          const int pos0 = 32 * c + 16 * s2 + 8 * half;
 #pragma unroll
           for (int dt = 0; dt < DT; ++dt) {
             const char* vrow = vs + (dt * 32 + col) * L::VROW;
-            const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow + key0 * 2);
-            const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + (key0 + 8) * 2);
-            o[dt] = mfma_bf16_32x32x16(u32x4{lo[0], lo[1], hi[0], hi[1]}, pb, o[dt]);
+            o[dt] = mfma_bf16_32x32x16(*reinterpret_cast<const u32x4*>(vrow + pos0 * 2), pb, o[dt]);
           }
         }
       l += psum;

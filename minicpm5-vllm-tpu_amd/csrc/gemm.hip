@@ -30,7 +30,7 @@ constexpr int BKB = 64;   // K bytes per LDS stage (two MFMA k-steps)
 template <int BM_, int BN_, int WGM_, int WGN_, int NST_, int OCC_, int LOOP_ = 0>
 struct GemmCfg {
   static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_, NST = NST_, OCC = OCC_;
-  // main loop: 0 split k-step pipeline, 1 ping-pong (two wave groups)
+  // main loop: 0 split k-step pipeline, 1 ping-pong (two wave groups, operand prefetch)
   static constexpr int LOOP = LOOP_;
   static constexpr int NW = WGM * WGN, NTH = 64 * NW;
   static constexpr int WM = BM / WGM, WN = BN / WGN;     // wave tile
@@ -41,7 +41,7 @@ struct GemmCfg {
   static_assert(BM % (16 * NW) == 0 && BN % (16 * NW) == 0, "load split");
   static_assert(NW * 32 * EROW <= NST * ST_BYTES, "epilogue staging fits in the ring");
   static_assert(WN % 64 == 0 || WN == 32, "wave tile width");
-  static_assert(LOOP != 1 || (WGM == 2 && NST >= 3), "ping-pong needs two wave groups and two stages in flight");
+  static_assert(LOOP == 0 || (WGM == 2 && NST >= 3), "ping-pong needs two wave groups and two stages in flight");
 };
 // 256x256 block, 128x128 per wave (accumulators in AGPRs), one workgroup per CU
 using CfgL = GemmCfg<256, 256, 2, 2, 3, 1, 0>;
@@ -258,50 +258,92 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
   // Materialize the epilogue's kernel arguments now: a scalar load still pending inside the loop would
   // turn every LDS wait there into lgkmcnt(0) (scalar loads return out of order).
   asm volatile("" ::"s"(g.out), "s"(g.res), "s"(g.rs), "s"(g.cs), "s"(g.aux), "s"(g.ldo), "s"(g.ldr));
-  u32x4 ra0[C::MT], rb0[C::NTL], ra1[C::MT], rb1[C::NTL];
   if constexpr (C::LOOP == 1) {
-    // Ping-pong: the waves form two groups (wm = 0, 1) with one wave of each on every SIMD.  Each
-    // iteration is a memory phase M (LDS reads of both k-steps of a stage into registers, async loads
-    // of the stage NST - 1 ahead) and a compute phase C (the stage's MFMAs), each closed by a barrier.
-    // Group 1 starts one barrier late, so on every SIMD one wave issues MFMAs while the other does its
-    // memory phase, and the barrier between phases never drains the MFMA pipe.  Group 0 waits for its
-    // own loads of stage s + 1 at the end of C(s), group 1 at the end of M(s): both before the barrier
-    // after which group 0 reads stage s + 1.  Every wave finishes its LDS reads before the barrier
-    // closing its M phase, so a stage's slot is refilled only after both groups have read it.
+    // Ping-pong.  The waves form two groups (wm = 0, 1) with one wave of each on every SIMD, and each
+    // iteration is a memory phase M (async loads of the stage NST - 1 ahead) and a compute phase C
+    // (the stage's MFMAs, with the next stage's operands read from LDS into registers alongside), each
+    // closed by a barrier.  Group 1 starts one barrier late, so on every SIMD one wave issues MFMAs
+    // while the other is in its memory phase or waiting at the barrier.
+    // Operands live in a ring of three k-step register sets: stage s uses (2s, 2s + 1) mod 3, and
+    // stage s + 1's k-step 0 goes to the free set, its k-step 1 to the set stage s's k-step 0 used.
+    // Stage s + 1 must be visible when group 0 starts C(s): group 0 waits for its loads of stage s + 1
+    // at the end of M(s), group 1 at the end of C(s - 1).  A stage's slot is refilled in M(s + 1) of
+    // the stage NST ahead, after both groups finished reading it in their C(s - 1).
     constexpr int D = C::NST - 1;
+    constexpr int NOP = C::MT + C::NTL;                   // operand registers per k-step: B then A
+    u32x4 H0[NOP], H1[NOP], H2[NOP];
+    auto rdq = [&](const char* Sb, int ks, int q, u32x4 (&dst)[NOP]) {
+      if (q < C::NTL) dst[q] = *reinterpret_cast<const u32x4*>(Sb + (ks ? bo1 : bo0) + q * 32 * BKB);
+      else dst[q] = *reinterpret_cast<const u32x4*>(Sb + (ks ? ao1 : ao0) + (q - C::NTL) * 32 * BKB);
+    };
+    auto mfq = [&](int i, const u32x4 (&src)[NOP]) {
+      const int mt = i / C::NTL, nt = i % C::NTL;
+      acc[mt][nt] = T::run(src[C::NTL + mt], src[nt], acc[mt][nt]);
+    };
+    // stages 0 and 1 visible; stage 0 in H0 / H1
+    if (nk >= D) MK_WAIT_VMCNT((D - 2) * Q);
+    else MK_WAIT_VMCNT(0);
+    lds_barrier();
+#pragma unroll
+    for (int q = 0; q < NOP; ++q) rdq(smem, 0, q, H0);
+#pragma unroll
+    for (int q = 0; q < NOP; ++q) rdq(smem, 1, q, H1);
+    __builtin_amdgcn_s_waitcnt(0xc07f);
     if (wm == 1) lds_barrier();
     int cur = 0;
-    for (int it = 0; it < nk; ++it) {
-      const char* S = smem + cur * C::ST_BYTES;
-      rd(S, ao0, bo0, ra0, rb0);
-      rd(S, ao1, bo1, ra1, rb1);
+    auto step = [&](int it, u32x4 (&ha)[NOP], u32x4 (&hb)[NOP], u32x4 (&hc)[NOP]) {
+      // M(it): async loads of stage it + D into the slot of stage it - 1
       const bool pre = it + D < nk;
       if (pre) {
         const int nslot = cur == 0 ? C::NST - 1 : cur - 1;
 #pragma unroll
         for (int j = 0; j < Q; ++j) issue1(j, nslot, (it + D) * BKB);
       }
-      __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's reads of the stage are done
-      if (wm == 1) {
+      if (wm == 0 && it + 1 < nk) {
         if (pre) MK_WAIT_VMCNT((D - 1) * Q);
         else MK_WAIT_VMCNT(0);
       }
       lds_barrier();
+      // C(it): MFMAs of stage it, reads of stage it + 1
+      const int s1 = cur == C::NST - 1 ? 0 : cur + 1;
+      const char* S1 = smem + s1 * C::ST_BYTES;
+      const bool nxt = it + 1 < nk;
       __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-      for (int i = 0; i < NMF; ++i) mf(i, ra0, rb0);
+      for (int i = 0; i < NMF; ++i) {
+        mfq(i, ha);
+        if (i < NOP && nxt) rdq(S1, 0, i, hc);
+        __builtin_amdgcn_sched_barrier(0);
+      }
 #pragma unroll
-      for (int i = 0; i < NMF; ++i) mf(i, ra1, rb1);
+      for (int q = NMF; q < NOP; ++q)
+        if (nxt) rdq(S1, 0, q, hc);
+#pragma unroll
+      for (int i = 0; i < NMF; ++i) {
+        mfq(i, hb);
+        if (i < NOP && nxt) rdq(S1, 1, i, ha);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int q = NMF; q < NOP; ++q)
+        if (nxt) rdq(S1, 1, q, ha);
       __builtin_amdgcn_s_setprio(0);
-      if (wm == 0) {
-        if (pre) MK_WAIT_VMCNT((D - 1) * Q);
+      __builtin_amdgcn_s_waitcnt(0xc07f);                 // lgkmcnt(0): stage it + 1 is in registers
+      if (wm == 1 && it + 2 < nk) {
+        if (pre) MK_WAIT_VMCNT((D - 2) * Q);
         else MK_WAIT_VMCNT(0);
       }
       lds_barrier();
-      cur = cur == C::NST - 1 ? 0 : cur + 1;
+      cur = s1;
+    };
+    for (int it = 0; it < nk; it += 3) {
+      step(it, H0, H1, H2);
+      if (it + 1 < nk) step(it + 1, H2, H0, H1);
+      if (it + 2 < nk) step(it + 2, H1, H2, H0);
     }
     if (wm == 0) lds_barrier();
   } else {
+    u32x4 ra0[C::MT], rb0[C::NTL], ra1[C::MT], rb1[C::NTL];
     rd(smem, ao0, bo0, ra0, rb0);
     int cur = 0;                                            // stage slot of iteration it
     constexpr int SPLIT = NMF / 4;                          // k-step 1 MFMAs issued before the barrier
@@ -529,7 +571,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_kernel(GemmArgs g) 
 int choose_cfg(const GemmArgs& g) {
   if (g.cfg >= 1 && g.cfg <= 4) return g.cfg;
   static const int forced = [] {
-    const char* e = std::getenv("MK_GEMM_CFG");   // tuning override: 1 | 2 | 3 | 4
+    const char* e = std::getenv("MK_GEMM_CFG");   // tuning override: 1 .. 4
     return e ? std::atoi(e) : 0;
   }();
   if (forced >= 1 && forced <= 4) return forced;
