@@ -208,3 +208,88 @@ def test_lm_head():
         out = ops.lm_head(hdn, w)
         ref = hdn.float() @ w.float().t()          # f32 torch reference for a floating-point kernel
         torch.testing.assert_close(out, ref, rtol=1e-4, atol=2e-4)
+
+
+def _pack_gu_scales(s_il, inter):
+    """Per-column scales of the chunk-interleaved gate/up matrix in the packed 32-column [gate | up] order."""
+    from minicpm5_mk.mk_weights import mlp_chunk
+
+    ic = mlp_chunk(inter)
+    p = torch.arange(2 * inter)
+    n = (p // 64) * 32 + p % 32
+    src = (n // ic) * 2 * ic + ((p // 32) % 2) * ic + n % ic
+    return s_il.reshape(-1)[src].contiguous()
+
+
+@pytest.mark.parametrize("smooth", [False, True])
+def test_decoder_block_int8(smooth):
+    """Quantised decoder block at its full size (8192 tokens, MiniCPM5-1B hd-96 shapes): fused RMSNorm +
+    QKV (mk_mlp.py:161-170), int8d O projection + bf16 residual (mk_jax.py:243-265, :394), fused MLP with
+    int8 gate/up and int8 down (mk_mlp.py:68-97).  X ~ N(0, 1) from seed 3, weights ~ N(0, 0.02) from
+    seed 0 quantised per output channel; activations per-token dynamic int8 with a = gamma (= 1), or
+    SmoothQuant a = 1 / s with s from X's and the weight's per-channel amax (mk_weights.py:229-252).
+    Checked stage by stage against the oracle's restatement of the same algebra: QKV within one bf16 ulp,
+    the O residual bit-exact, the block output within bf16 rounding (SiLU's exp differs in the last f32
+    bits, which can move an int8 code of h)."""
+    from minicpm5_mk import ops
+    from minicpm5_mk.mk_weights import interleave_gu, mlp_chunk, quantize_w
+    from oracle import emulate
+
+    dev = _dev()
+    T, H, hd, n_q, n_kv, inter, eps = 8192, 1536, 96, 16, 2, 4608, 1e-6
+    D, qd = (n_q + 2 * n_kv) * hd, n_q * hd
+    print(f"[block] T={T} smooth={smooth}", flush=True)
+    x = torch.randn(T, H, generator=torch.Generator().manual_seed(3)).to(BF16)
+    g0 = torch.Generator().manual_seed(0)
+    w_qkv, w_o, w_gu, w_dn = (torch.randn(r, c, generator=g0) * 0.02 for r, c in
+                              ((H, D), (qd, H), (H, 2 * inter), (inter, H)))
+    ones = lambda n: torch.ones(n)  # noqa: E731
+
+    def smooth_of(xa, w):
+        if not smooth:
+            return ones(w.shape[0])
+        s = xa.float().abs().amax(0).pow(0.5) / w.abs().amax(1).clamp_min(1e-12).pow(0.5)
+        return s.clamp(1e-4, 1e4)
+
+    s1 = smooth_of(x, w_qkv)
+    q_qkv, sc_qkv = quantize_w(w_qkv * s1[:, None], "int8d", 1.0)
+    a_qkv = 1.0 / s1
+    q_o, sc_o = quantize_w(w_o, "int8d", 1.0)
+    q_gu, sc_gu = quantize_w(w_gu * s1[:, None], "int8d", 1.0)
+    q_dn, sc_dn = quantize_w(w_dn, "int8d", 1.0)
+    ic = mlp_chunk(inter)
+    q_gu_il, sc_gu_il = interleave_gu(q_gu.view(H, 2, inter), sc_gu.view(2, inter), ic)
+    a_o, a_dn = ones(qd), ones(inter)
+
+    # ---- GPU, launched as the model's layer does
+    xd = x.to(dev)
+    q8, sx = ops.row_quant(xd, a_qkv.to(dev), eps, True, True)
+    qkv = ops.gemm(q8, ops.pack_weight(q_qkv.to(dev)), "dq_bf16", rs=sx, cs=sc_qkv.reshape(-1).to(dev))
+    att = qkv[:, :qd].contiguous()          # stands in for the attention output (same shape)
+    q8, sx = ops.row_quant(att, a_o.to(dev), 0.0, False, False)
+    x1 = ops.gemm(q8, ops.pack_weight(q_o.to(dev)), "dq_res_bf16add", rs=sx, cs=sc_o.reshape(-1).to(dev),
+                  res=xd.clone())
+    q8, sx = ops.row_quant(x1, a_qkv.to(dev), eps, True, True)
+    wgu = ops.pack_weight(q_gu_il.to(dev), map_gu=True, ic=ic, inter=inter)
+    h = ops.gemm(q8, wgu, "dq_silu_f32a", rs=sx, cs=_pack_gu_scales(sc_gu_il, inter).to(dev), aux=a_dn.to(dev))
+    q8, sx = ops.row_quant(h, None, 0.0, False, True)
+    x2 = ops.gemm(q8, ops.pack_weight(q_dn.to(dev)), "dq2_res_f32add", rs=sx, cs=sc_dn.reshape(-1).to(dev),
+                  res=x1.clone())
+    torch.cuda.synchronize()
+    qkv, x1, x2 = qkv.cpu(), x1.cpu(), x2.float().cpu()
+
+    # ---- oracle, stage by stage on the GPU's own inputs to each stage.  RMSNorm's sum of squares runs
+    # in a different order on the GPU, so rstd (and the dequantised QKV / gate-up values) may differ by
+    # one f32 ulp: QKV within one bf16 ulp, the O stage bit-exact
+    def within_ulp(a, b):   # one bf16 ulp is at most 2^-7 of the value
+        return bool(((a.float() - b.float()).abs() <= b.float().abs() * 2.0 ** -7 + 1e-30).all())
+
+    qkv_r = emulate.fused_qkv(x, q_qkv, sc_qkv, a_qkv, eps)
+    assert within_ulp(qkv, qkv_r)
+    o_r = emulate.linear(qkv[:, :qd], q_o, sc_o, a_o, "int8d")
+    x1_r = emulate.bf(x.float() + o_r.float()).to(BF16)
+    assert torch.equal(x1, x1_r)
+    x2_r = emulate.fused_mlp(x1, q_gu_il, sc_gu_il, a_qkv, q_dn, sc_dn, a_dn, eps, ic).float()
+    err = (x2 - x2_r).abs()
+    print(f"[block] out max {err.max():.4g} mean {err.mean():.4g}; |out| max {x2_r.abs().max():.3g}", flush=True)
+    assert (err <= x2_r.abs() * 2.0 ** -7 + 2e-2).all() and err.mean() <= 1e-3, (float(err.max()), float(err.mean()))
