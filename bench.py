@@ -7,10 +7,13 @@ value = B * 8192 / mean step latency (tokens/s); p50 latency uses linear interpo
 (benchmark/run_benchmark.py:186-194, :437-440 of the reference).
 
 Extra fields:
-  roofline      the attention kernel (dominant kernel of the step) timed alone with HIP events on its
-                launch stream at the step's shape; algorithmic FLOPs = 4 hd n_q S(S+1)/2 per sequence
-                and layer, peak = MI355X dense bf16 2.5 PFLOP/s.
-  kernels       the same for the QKV / gate-up (int8 MFMA, peak 5.0 POP/s) and O / down (bf16) GEMMs.
+  roofline      the attention kernel (dominant kernel of the step) inside the model: after the timed
+                loop one eager forward of the same shape runs with a HIP event pair around every launch
+                on the model's stream (mk_forward_timed); achieved = algorithmic FLOPs per launch
+                (4 hd n_q S(S+1)/2 per sequence and layer) / average launch time, peak = MI355X dense
+                bf16 2.5 PFLOP/s.
+  kernels       the same for every kernel category: QKV / gate-up GEMMs (int8 MFMA, peak 5.0 POP/s when
+                quantised), O / down (bf16 unless quantised), the row kernels and the LM head (HBM GB/s).
   cpu_baseline  the oracle's FP32 CPU forward (oracle/golden.py, a restatement of the reference's
                 FP32 golden) timed on a bounded sample -- the first --cpu-layers layers of one
                 8192-token sequence -- and scaled to the full model (layers + LM head).
@@ -137,6 +140,44 @@ def kernel_roofline(cfg, B, S, iters=20):
     return res
 
 
+def model_roofline(eng, cfg, ids):
+    """Per-kernel-category time of one eager forward (mk_forward_timed) -> achieved rate vs MI355X peak."""
+    from minicpm5_mk.quant import parse_quant
+
+    B, S = ids.shape
+    T = B * S
+    H, I, hd, nq, nkv, V = cfg.hidden, cfg.inter, cfg.head_dim, cfg.n_q, cfg.n_kv, cfg.vocab
+    qm = parse_quant(eng.quant)
+    i8 = {k: qm[k] == "int8d" for k in ("qkv", "o", "gu", "down")}
+    flat = ids.reshape(-1)
+    eng.model.forward_timed(flat, B, S, logits=True)          # first eager pass: code objects, caches
+    t = eng.model.forward_timed(flat, B, S, logits=True)
+    work = {   # kind -> (algorithmic units per launch, unit, peak)
+        "attn": (4.0 * hd * nq * S * (S + 1) / 2 * B, "TFLOP/s", PEAK["bf16"]),
+        "gemm_qkv": (2.0 * T * H * (nq + 2 * nkv) * hd, "TOP/s" if i8["qkv"] else "TFLOP/s",
+                     PEAK["int8" if i8["qkv"] else "bf16"]),
+        "gemm_o": (2.0 * T * nq * hd * H, "TOP/s" if i8["o"] else "TFLOP/s", PEAK["int8" if i8["o"] else "bf16"]),
+        "gemm_gu": (2.0 * T * H * 2 * I, "TOP/s" if i8["gu"] else "TFLOP/s", PEAK["int8" if i8["gu"] else "bf16"]),
+        "gemm_down": (2.0 * T * I * H, "TOP/s" if i8["down"] else "TFLOP/s", PEAK["int8" if i8["down"] else "bf16"]),
+        # K and V read and written once: 4 S kv_dim bf16 bytes per sequence
+        "attn_prep": (4.0 * T * nkv * hd * 2, "GB/s", PEAK["hbm"]),
+        # per-token int8 quantisation of an H-wide bf16 row: 2 H read, H written, 4 B scale
+        "norm": (T * (3.0 * H + 4), "GB/s", PEAK["hbm"]),
+        "lm_head": (2.0 * V * H, "GB/s", PEAK["hbm"]),        # the bf16 weight read
+    }
+    out = {}
+    for k, (ms, n) in t.items():
+        if n == 0:
+            continue
+        e = {"avg_us": round(ms * 1e3 / n, 2), "launches": n, "total_ms": round(ms, 3)}
+        if k in work:
+            units, unit, peak = work[k]
+            rate = units / (ms / n) / (1e6 if unit == "GB/s" else 1e9)   # units per ms -> GB/s or T(FL)OP/s
+            e.update({"achieved": round(rate, 1), "unit": unit, "peak": peak, "frac": round(rate / peak, 4)})
+        out[k] = e
+    return out
+
+
 def cpu_baseline(cfg, n_layers, seq=8192):
     """The oracle's FP32 forward (restating benchmark/f32_golden.py) on `n_layers` layers of one
     sequence, scaled to the full model: layers x L / n_layers + the LM head."""
@@ -229,15 +270,16 @@ def main():
 
     main_run = run(args.batch, args.steps, args.warmup)
     log(f"[bench] B={args.batch}: {main_run}")
+    kern = None
+    if not args.no_kernels:
+        kern = model_roofline(eng, cfg, random_token_ids(args.batch, args.seq, seed=1234).to("cuda:0"))
+        log(f"[bench] in-model kernels: {json.dumps(kern)}")
     sweep = []
     for b in [int(x) for x in args.sweep.split(",") if x.strip()]:
         r = run(b, max(3, min(args.steps, int(80 / b))), 1)
         log(f"[bench] sweep B={b}: {r}")
         sweep.append(r)
     eng.model.release_buffers()
-    kern = None if args.no_kernels else kernel_roofline(cfg, args.batch, args.seq)
-    if kern:
-        log(f"[bench] kernels: {json.dumps(kern)}")
     eng.close()
     del eng
     torch.cuda.empty_cache()
@@ -257,12 +299,11 @@ def main():
         "tflops_reference_formula": round(main_run["tflops_reference_formula"], 1),
     }
     if kern:
-        a = kern["attention"]
-        out["roofline"] = {"bound": "mfma", "achieved": round(a["tflops"], 1), "peak": PEAK["bf16"], "unit": "TFLOP/s",
-                           "frac": round(a["frac"], 4), "traffic": None, "kernel": "attn_fwd_kernel",
-                           "avg_ms": round(a["ms"], 4)}
-        out["kernels"] = {k: {"avg_ms": round(v["ms"], 4), "tflops": round(v["tflops"], 1), "frac": round(v["frac"], 4)}
-                          for k, v in kern.items()}
+        a = kern["attn"]
+        out["roofline"] = {"bound": "mfma", "achieved": a["achieved"], "peak": a["peak"], "unit": a["unit"],
+                           "frac": a["frac"], "traffic": None, "kernel": "attn_fwd_kernel",
+                           "avg_ms": round(a["avg_us"] / 1e3, 4), "timing": "in-model, HIP events per launch"}
+        out["kernels"] = kern
     if cpu:
         out["cpu_baseline"] = cpu
     if sweep:

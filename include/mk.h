@@ -116,6 +116,29 @@ int mk_forward(mk_model* m, const int32_t* input_ids, int bs, int seq, void* hid
 /* 1 (default) replays captured hipGraphs, 0 launches kernels eagerly on every call. */
 int mk_set_graph_mode(mk_model* m, int enable);
 
+/* Kernel categories of mk_forward_timed. */
+enum {
+  MK_KERNEL_EMBED = 0,      /* embedding gather */
+  MK_KERNEL_NORM = 1,       /* RMSNorm / per-token int8 quantisation row kernels */
+  MK_KERNEL_GEMM_QKV = 2,   /* QKV projection */
+  MK_KERNEL_ATTN_PREP = 3,  /* K RoPE + V transpose */
+  MK_KERNEL_ATTN = 4,       /* causal GQA flash attention */
+  MK_KERNEL_GEMM_O = 5,     /* O projection + residual */
+  MK_KERNEL_GEMM_GU = 6,    /* gate/up projection + SiLU * up */
+  MK_KERNEL_GEMM_DOWN = 7,  /* down projection + residual */
+  MK_KERNEL_LAST = 8,       /* last layer (last token only) + final norm */
+  MK_KERNEL_LM_HEAD = 9,    /* LM head */
+  MK_KERNEL_OTHER = 10,
+  MK_KERNEL_KINDS = 11
+};
+
+/* mk_forward launched eagerly with a hipEvent pair around every kernel: ms[k] = summed kernel time
+ * and launches[k] = launch count of category k (arrays of MK_KERNEL_KINDS).  Synchronizes `stream`.
+ * No counterpart in the reference: the per-kernel, in-model timing behind the benchmark's roofline. */
+int mk_forward_timed(mk_model* m, const int32_t* input_ids, int bs, int seq, void* hidden_out,
+                     float* logits_out, void* workspace, size_t workspace_bytes, void* stream, float* ms,
+                     int* launches);
+
 /* ---------------------------------------------------------------- kernel-level entry points */
 
 /* Causal GQA prefill attention (super_gqa_v2, mk_attn.py:660-710): qkv (B, S, (n_q + 2 n_kv) hd) bf16

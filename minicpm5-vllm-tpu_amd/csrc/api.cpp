@@ -118,6 +118,13 @@ int mk_forward(mk_model* m, const int32_t* input_ids, int bs, int seq, void* hid
                            static_cast<hipStream_t>(stream)));
 }
 
+int mk_forward_timed(mk_model* m, const int32_t* input_ids, int bs, int seq, void* hidden_out, float* logits_out,
+                     void* workspace, size_t workspace_bytes, void* stream, float* ms, int* launches) {
+  MK_REQUIRE(m != nullptr, "forward_timed: null model");
+  MK_TRY(mk::model_forward_timed(m->impl, input_ids, bs, seq, hidden_out, logits_out, workspace, workspace_bytes,
+                                 static_cast<hipStream_t>(stream), ms, launches));
+}
+
 int mk_set_graph_mode(mk_model* m, int enable) {
   MK_REQUIRE(m != nullptr, "set_graph_mode: null model");
   m->impl->use_graph = enable != 0;

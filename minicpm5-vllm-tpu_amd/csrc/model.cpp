@@ -254,6 +254,18 @@ Model::~Model() {
 
 namespace {
 
+// Per-kind kernel timing of an eager forward: an event pair around every launch, summed per kind.
+struct KernelTimer {
+  struct Mark { int kind; hipEvent_t a, b; };
+  std::vector<Mark> marks;
+  ~KernelTimer() {
+    for (auto& k : marks) {
+      hipEventDestroy(k.a);
+      hipEventDestroy(k.b);
+    }
+  }
+};
+
 struct Fwd {
   const Model& m;
   const int32_t* ids;
@@ -262,6 +274,7 @@ struct Fwd {
   float* logits;
   char* ws;
   WorkLayout W;
+  KernelTimer* tm = nullptr;
 };
 
 int launch_forward(const Fwd& f, hipStream_t st) {
@@ -285,12 +298,26 @@ int launch_forward(const Fwd& f, hipStream_t st) {
   const size_t e0 = esz(q.i8[0]), e1 = esz(q.i8[1]), e2 = esz(q.i8[2]), e3 = esz(q.i8[3]);
   const bool d8 = q.fmlp && q.i8[3];
   int rc;
-#define MK_RUN(call)     \
-  do {                   \
-    rc = (call);         \
-    if (rc) return rc;   \
+  int kind = MK_KERNEL_OTHER;   // timing category of the launches that follow
+#define MK_RUN(call)                                                   \
+  do {                                                                 \
+    KernelTimer::Mark mk_{kind, nullptr, nullptr};                     \
+    if (f.tm) {                                                        \
+      MK_HIP_CHECK(hipEventCreate(&mk_.a));                            \
+      if (hipEventCreate(&mk_.b) != hipSuccess) {                      \
+        hipEventDestroy(mk_.a);                                        \
+        set_error("forward: hipEventCreate failed");                   \
+        return MK_EHIP;                                                \
+      }                                                                \
+      f.tm->marks.push_back(mk_);                                      \
+      MK_HIP_CHECK(hipEventRecord(mk_.a, st));                         \
+    }                                                                  \
+    rc = (call);                                                       \
+    if (rc) return rc;                                                 \
+    if (f.tm) MK_HIP_CHECK(hipEventRecord(mk_.b, st));                 \
   } while (0)
 
+  kind = MK_KERNEL_EMBED;
   MK_RUN(launch_embed(f.ids, static_cast<const uint16_t*>(m.w.embed), x, T, H, c.vocab, st));
 
   for (int l = 0; l < Lm; ++l) {
@@ -306,6 +333,7 @@ int launch_forward(const Fwd& f, hipStream_t st) {
     g.B = pb + m.P.wqkv + (size_t)l * D * H * e0;
     if (q.i8[0]) {
       QuantArgs qa{x, H, false, m.w.a_qkv + (size_t)l * H, T, H, c.eps, true, q.fqkv, xq, H, sx};
+      kind = MK_KERNEL_NORM;
       MK_RUN(launch_rowquant(qa, st));
       g.in = GemmIn::I8;
       g.A = xq;
@@ -313,11 +341,13 @@ int launch_forward(const Fwd& f, hipStream_t st) {
       g.cs = m.w.s_qkv + (size_t)l * D;
       g.epi = q.fqkv ? Epi::DQ_BF16 : Epi::DQ2_BF16;
     } else {
+      kind = MK_KERNEL_NORM;
       MK_RUN(launch_rmsnorm_bf16(x, H, nullptr, xn, H, T, H, c.eps, st));
       g.in = GemmIn::BF16;
       g.A = xn;
       g.epi = Epi::BF16;
     }
+    kind = MK_KERNEL_GEMM_QKV;
     MK_RUN(launch_gemm(g, st));
 
     // ---- causal GQA attention (super_gqa_v2); sm_scale is folded into W_q (mk_weights.py:147)
@@ -334,7 +364,10 @@ int launch_forward(const Fwd& f, hipStream_t st) {
     aa.n_kv = c.n_kv;
     aa.hd = c.head_dim;
     aa.qscale = 1.4426950408889634f;
-    MK_RUN(launch_attn(aa, st));
+    kind = MK_KERNEL_ATTN_PREP;
+    MK_RUN(launch_attn_stages(aa, st, 1));
+    kind = MK_KERNEL_ATTN;
+    MK_RUN(launch_attn_stages(aa, st, 2));
 
     // ---- O projection + residual (mk_jax.py:394)
     GemmArgs go{};
@@ -348,6 +381,7 @@ int launch_forward(const Fwd& f, hipStream_t st) {
     go.B = pb + m.P.wo + (size_t)l * H * qd * e1;
     if (q.i8[1]) {
       QuantArgs qa{attn, qd, false, m.w.a_o + (size_t)l * qd, T, qd, c.eps, false, false, xq, qd, sx};
+      kind = MK_KERNEL_NORM;
       MK_RUN(launch_rowquant(qa, st));
       go.in = GemmIn::I8;
       go.A = xq;
@@ -359,6 +393,7 @@ int launch_forward(const Fwd& f, hipStream_t st) {
       go.A = attn;
       go.epi = Epi::RES_BF16ADD;
     }
+    kind = MK_KERNEL_GEMM_O;
     MK_RUN(launch_gemm(go, st));
 
     // ---- MLP (_mlp_block, mk_jax.py:408-423): fused kernel algebra with fmlp, XLA algebra otherwise
@@ -373,6 +408,7 @@ int launch_forward(const Fwd& f, hipStream_t st) {
     gu.B = pb + m.P.wgu + (size_t)l * 2 * I * H * e2;
     if (q.i8[2]) {
       QuantArgs qa{x, H, false, m.w.a_gu + (size_t)l * H, T, H, c.eps, true, q.fmlp, xq, H, sx};
+      kind = MK_KERNEL_NORM;
       MK_RUN(launch_rowquant(qa, st));
       gu.in = GemmIn::I8;
       gu.A = xq;
@@ -381,11 +417,13 @@ int launch_forward(const Fwd& f, hipStream_t st) {
       gu.epi = q.fmlp ? (d8 ? Epi::DQ_SILU_F32A : Epi::DQ_SILU) : Epi::SILU_BF16;
       if (d8) gu.aux = m.w.a_down + (size_t)l * I;
     } else {
+      kind = MK_KERNEL_NORM;
       MK_RUN(launch_rmsnorm_bf16(x, H, nullptr, xn, H, T, H, c.eps, st));
       gu.in = GemmIn::BF16;
       gu.A = xn;
       gu.epi = Epi::SILU_BF16;
     }
+    kind = MK_KERNEL_GEMM_GU;
     MK_RUN(launch_gemm(gu, st));
 
     GemmArgs gd{};
@@ -400,6 +438,7 @@ int launch_forward(const Fwd& f, hipStream_t st) {
       // fused int8 down (mk_mlp.py:85-95) quantises h * a_down (already applied) with u * (1/s);
       // the XLA int8d linear quantises h * a_down with u / s (mk_jax.py:257-262)
       QuantArgs qa{h, I, d8, d8 ? nullptr : m.w.a_down + (size_t)l * I, T, I, c.eps, false, d8, xq, I, sx};
+      kind = MK_KERNEL_NORM;
       MK_RUN(launch_rowquant(qa, st));
       gd.in = GemmIn::I8;
       gd.A = xq;
@@ -413,8 +452,10 @@ int launch_forward(const Fwd& f, hipStream_t st) {
       gd.lda = I;
       gd.epi = q.fmlp ? Epi::RES_F32ADD : Epi::RES_BF16ADD;
     }
+    kind = MK_KERNEL_GEMM_DOWN;
     MK_RUN(launch_gemm(gd, st));
   }
+  kind = MK_KERNEL_LAST;
 
   // ---- last layer, exact for the last token only (last_layer_step, mk_jax.py:492-520), bf16
   uint16_t* kvall = qkv;
@@ -528,6 +569,7 @@ int launch_forward(const Fwd& f, hipStream_t st) {
   const int rows_out = std::max(8, B);
   if (rows_out > B) MK_RUN(launch_zero(f.hidden + (size_t)B * H, (size_t)(rows_out - B) * H * 2, st));
   MK_RUN(launch_rmsnorm_bf16(xl, H, static_cast<const uint16_t*>(m.w.final_norm), f.hidden, H, B, H, c.eps, st));
+  kind = MK_KERNEL_LM_HEAD;
   if (f.logits) {
     for (int b0 = 0; b0 < B; b0 += 32) {
       const int rows = std::min(32, B - b0);
@@ -557,6 +599,35 @@ int validate_run(const mk_config& c, int bs, int seq) {
   MK_REQUIRE(seq >= 256 && seq % 256 == 0, "forward: seq must be a positive multiple of 256");
   MK_REQUIRE(seq <= c.max_seq, "forward: seq exceeds the RoPE table rows (max_seq)");
   MK_REQUIRE((long long)bs * seq <= (1LL << 30), "forward: bs * seq too large");
+  return MK_OK;
+}
+
+int model_forward_timed(Model* m, const int32_t* ids, int bs, int seq, void* hidden, float* logits, void* ws,
+                        size_t ws_bytes, hipStream_t st, float* ms, int* launches) {
+  MK_REQUIRE(m != nullptr, "forward_timed: null model");
+  MK_REQUIRE(ms != nullptr && launches != nullptr, "forward_timed: null outputs");
+  int rc = validate_run(m->cfg, bs, seq);
+  if (rc) return rc;
+  MK_REQUIRE(ids && hidden && ws, "forward_timed: null ids / output / workspace");
+  MK_REQUIRE(!logits || m->w.lm_head, "forward_timed: logits requested but the model has no lm_head");
+  WorkLayout W{};
+  workspace_layout(*m, bs, seq, &W);
+  MK_REQUIRE(ws_bytes >= W.total, "forward_timed: workspace too small");
+  KernelTimer tm;
+  Fwd f{*m, ids, bs, seq, static_cast<uint16_t*>(hidden), logits, static_cast<char*>(ws), W, &tm};
+  rc = launch_forward(f, st);
+  if (rc) return rc;
+  MK_HIP_CHECK(hipStreamSynchronize(st));
+  for (int k = 0; k < MK_KERNEL_KINDS; ++k) {
+    ms[k] = 0.f;
+    launches[k] = 0;
+  }
+  for (auto& k : tm.marks) {
+    float t = 0.f;
+    MK_HIP_CHECK(hipEventElapsedTime(&t, k.a, k.b));
+    ms[k.kind] += t;
+    launches[k.kind] += 1;
+  }
   return MK_OK;
 }
 

@@ -61,6 +61,10 @@ int packed_layout(const mk_config* c, const QuantPlan& q, PackedLayout* L);
 int workspace_layout(const Model& m, int B, int S, WorkLayout* W);
 int model_create(const mk_config* cfg, const char* quant, const mk_weights* w, void* packed, size_t packed_bytes,
                  hipStream_t st, Model** out);
+// Eager forward with an event pair around every launch: per-kind kernel time (ms) and launch counts,
+// indexed by MK_KERNEL_*.  Synchronizes the stream.
+int model_forward_timed(Model* m, const int32_t* ids, int bs, int seq, void* hidden, float* logits, void* ws,
+                        size_t ws_bytes, hipStream_t st, float* ms, int* launches);
 int model_forward(Model* m, const int32_t* ids, int bs, int seq, void* hidden, float* logits, void* ws,
                   size_t ws_bytes, hipStream_t st);
 

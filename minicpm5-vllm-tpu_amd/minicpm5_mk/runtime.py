@@ -152,6 +152,29 @@ class MkModel:
                 return hidden
             return hidden, (lg.clone() if copy_out else lg)
 
+    KERNEL_KINDS = ("embed", "norm", "gemm_qkv", "attn_prep", "attn", "gemm_o", "gemm_gu", "gemm_down", "last_layer",
+                    "lm_head", "other")   # MK_KERNEL_* order (include/mk.h)
+
+    def forward_timed(self, input_ids: torch.Tensor, bs: int, seq: int, logits: bool = False) -> dict:
+        """One eager forward with a hipEvent pair around every kernel launch: {kind: (ms, launches)}
+        (synchronizes the current stream)."""
+        if logits and not self.has_lm_head:
+            raise MkError("logits requested but the model was built without lm_head")
+        if input_ids.numel() < bs * seq or not input_ids.is_cuda:
+            raise MkError("input_ids must be a GPU tensor of >= bs*seq tokens")
+        n = len(self.KERNEL_KINDS)
+        ms, cnt = (ctypes.c_float * n)(), (ctypes.c_int * n)()
+        with self._lock:
+            b = self._buffers(bs, seq, logits)
+            b["ids"].copy_(input_ids.reshape(-1)[: bs * seq])
+            lg = b["logits"]
+            check(load().mk_forward_timed(self._h, ctypes.c_void_p(b["ids"].data_ptr()), bs, seq,
+                                          ctypes.c_void_p(b["hidden"].data_ptr()),
+                                          ctypes.c_void_p(lg.data_ptr()) if lg is not None else None,
+                                          ctypes.c_void_p(b["ws"].data_ptr()), b["ws"].numel(), _stream(), ms, cnt),
+                  "mk_forward_timed")
+        return {k: (ms[i], cnt[i]) for i, k in enumerate(self.KERNEL_KINDS)}
+
     def close(self) -> None:
         if getattr(self, "_h", None):
             load().mk_model_destroy(self._h)

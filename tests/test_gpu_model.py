@@ -145,3 +145,24 @@ def test_batch_invariance_and_graph_replay():
     for o in outs:
         assert torch.equal(o, eager)
     m.close()
+
+
+def test_forward_timed_matches_forward():
+    """mk_forward_timed: same result as the graph-replayed forward, one launch per layer per kernel kind."""
+    from minicpm5_mk.config import preset
+    from minicpm5_mk.synth import random_hf_state_dict, random_token_ids
+
+    dev = _dev()
+    cfg = preset("tiny")
+    sd = random_hf_state_dict(cfg)
+    m, _ = _build(cfg, "int8d:qkv+gu|sq|lastbf16|fqkv|fmlp", sd, 1024, dev)
+    ids = random_token_ids(2, 512, seed=5).to(dev)
+    h, lg = m.forward(ids.reshape(-1), 2, 512, logits=True)
+    t = m.forward_timed(ids.reshape(-1), 2, 512, logits=True)
+    h2, lg2 = m.forward(ids.reshape(-1), 2, 512, logits=True, copy_out=False)   # buffers the timed run wrote
+    L = cfg.num_layers - 1
+    assert t["attn"][1] == L and t["attn_prep"][1] == L and t["gemm_qkv"][1] == L and t["gemm_gu"][1] == L
+    assert t["embed"][1] == 1 and t["lm_head"][1] >= 1
+    assert all(ms >= 0.0 for ms, _ in t.values()) and t["attn"][0] > 0.0
+    assert torch.equal(h, h2) and torch.equal(lg, lg2)
+    m.close()
