@@ -33,6 +33,9 @@ sys.path[:0] = [ROOT, os.path.join(ROOT, "minicpm5-vllm-tpu_amd")]
 
 PEAK = {"bf16": 2516.6, "int8": 5033.2, "hbm": 8000.0}   # MI355X dense TFLOP/s, TOP/s; HBM GB/s
 METRIC = "prefill tokens/sec at (B,8192) B=1..32, 1B and 2B arch; p50 ms at (1,8192)"
+# HBM bytes per attn_fwd_kernel launch measured by rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (scaled by a
+# 256 MiB copy's counters) for the default workload; profiles/mfma_util_hbm_1b_b1_s8192.txt
+ATTN_TRAFFIC = {("1b", 1, 8192, "auto"): (96.5e6 + 44.0e6)}
 
 
 def log(*a):
@@ -301,7 +304,9 @@ def main():
     if kern:
         a = kern["attn"]
         out["roofline"] = {"bound": "mfma", "achieved": a["achieved"], "peak": a["peak"], "unit": a["unit"],
-                           "frac": a["frac"], "traffic": None, "kernel": "attn_fwd_kernel",
+                           "frac": a["frac"],
+                           "traffic": ATTN_TRAFFIC.get((args.arch, args.batch, args.seq, args.quant)),
+                           "kernel": "attn_fwd_kernel",
                            "avg_ms": round(a["avg_us"] / 1e3, 4), "timing": "in-model, HIP events per launch"}
         out["kernels"] = kern
     if cpu:
