@@ -283,16 +283,83 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
     qk(0, scur);
     rowmax_rescale(0, scur);
 
-    // ---- steady state: iteration t issues QK(t+1), softmax + PV(t), and stages K(t+2), V(t+1)
+    // ---- steady state: iteration t computes QK(t+1), softmax + PV(t) and stages K(t+2), V(t+1).
+    // The two waves of a SIMD run in step (one barrier per tile), so a wave overlaps its own VALU
+    // work with its MFMAs: the QK(t+1) MFMAs are issued with the softmax of tile t (exp2, bf16 P,
+    // row sum) interleaved, the PV(t) MFMAs with the row max of tile t+1 interleaved.  Each step is
+    // one MFMA plus a slice of the VALU work; LDS operands are read PF steps ahead.
+    constexpr int NQK = 2 * KS, NPV = 4 * DT, NCH = 16, PF = 3;
     for (int t = 0; t + 1 < nkt; ++t) {
       gload_k(min(t + 2, nkt - 1));   // the clamped reload at the end lands in a free slot
       gload_v(t + 1);
-      qk((t + 1) % L::NK, snext);
-      softmax_pv(t % L::NV, scur);
+      const char* ksl = kring + ((t + 1) % L::NK) * L::KBYTES;
+      auto kread = [&](int j) {
+        const int s = j / 2, c = j % 2;
+        return *reinterpret_cast<const u32x4*>(ksl + (32 * c + col) * L::KROW + (16 * s + 8 * half) * 2);
+      };
+      u32x4 kr[NQK];
+      u32x4 pb[2][2];
+      float psum = 0.f;
+      snext[0] = f32x16{};
+      snext[1] = f32x16{};
+#pragma unroll
+      for (int j = 0; j < PF; ++j) kr[j] = kread(j);
+#pragma unroll
+      for (int j = 0; j < NQK; ++j) {
+        if (j + PF < NQK) kr[j + PF] = kread(j + PF);
+        snext[j % 2] = mfma_bf16_32x32x16(kr[j], qreg[j / 2], snext[j % 2]);
+#pragma unroll
+        for (int k = j * NCH / NQK; k < (j + 1) * NCH / NQK; ++k) {
+          const int c = k / 8, s2 = (k / 4) % 2, e = k % 4;
+          const float p0 = fast_exp2(scur[c][8 * s2 + 2 * e] - m);
+          const float p1 = fast_exp2(scur[c][8 * s2 + 2 * e + 1] - m);
+          pb[c][s2][e] = pack_bf2(p0, p1);
+          psum = dot2_bf16_sum(pb[c][s2][e], psum);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      const int k0 = (t + 1) * KT;
+      if (k0 + KT - 1 > t0) {
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = k0 + 32 * c + 8 * (r >> 2) + 4 * half + (r & 3);
+            if (key > tok) snext[c][r] = -INFINITY;
+          }
+      }
+      const char* vsl = vring + (t % L::NV) * L::VBYTES;
+      auto vread = [&](int j) {
+        const int c = j / (2 * DT), s2 = (j / DT) % 2, dt = j % DT;
+        return *reinterpret_cast<const u32x4*>(vsl + (dt * 32 + col) * L::VROW + (32 * c + 16 * s2 + 8 * half) * 2);
+      };
+      u32x4 vr[NPV];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < PF; ++j) vr[j] = vread(j);
+#pragma unroll
+      for (int j = 0; j < NPV; ++j) {
+        if (j + PF < NPV) vr[j + PF] = vread(j + PF);
+        const int c = j / (2 * DT), s2 = (j / DT) % 2, dt = j % DT;
+        o[dt] = mfma_bf16_32x32x16(vr[j], pb[c][s2], o[dt]);
+#pragma unroll
+        for (int k = j * NCH / NPV; k < (j + 1) * NCH / NPV; ++k)
+          mx = fmaxf(mx, fmaxf(snext[k / 8][2 * (k % 8)], snext[k / 8][2 * (k % 8) + 1]));
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      l += psum;
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      if (__any(mx > m + RESCALE_T)) {
+        const float mnew = fmaxf(m, mx);
+        const float alpha = fast_exp2(m - mnew);
+        l *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+        m = mnew;
+      }
       sstore_k((t + 2) % L::NK);
       sstore_v((t + 1) % L::NV);
       __syncthreads();
-      rowmax_rescale(t + 1, snext);
       scur[0] = snext[0];
       scur[1] = snext[1];
     }

@@ -14,6 +14,7 @@
 //                  mk_mlp.py:95-96     out = bf16(x + acc * (s_h * s_d))   (int8 W_down)
 //   linear         mk_jax.py:243,265   bf16(acc) / bf16((acc * s_x) * s_w), then bf16 residual
 //                                      add x + o (mk_jax.py:394)
+#include <algorithm>
 #include <cmath>
 #include <cstdlib>
 
@@ -149,7 +150,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
   const int ntn = gridDim.x, ntm = gridDim.y, nblk = gridDim.x * gridDim.y;
   const int lid = blockIdx.x + ntn * blockIdx.y;
   const int work = (nblk % 8 == 0) ? (lid % 8) * (nblk / 8) + lid / 8 : lid;
-  constexpr int GM = 8;
+  const int GM = g.gm;
   const int grp = work / (GM * ntn), first_m = grp * GM, gsz = min(ntm - first_m, GM);
   const int wig = work - grp * GM * ntn;
   const int m0 = (first_m + wig % gsz) * C::BM, n0 = (wig / gsz) * C::BN;
@@ -594,8 +595,17 @@ int choose_cfg(const GemmArgs& g) {
 }
 
 template <class C, GemmIn IN, Epi EPI>
-void launch_c(const GemmArgs& g, hipStream_t st) {
-  dim3 grid((g.N + C::BN - 1) / C::BN, (g.M + C::BM - 1) / C::BM);
+void launch_c(const GemmArgs& g0, hipStream_t st) {
+  dim3 grid((g0.N + C::BN - 1) / C::BN, (g0.M + C::BM - 1) / C::BM);
+  GemmArgs g = g0;
+  if (g.gm <= 0) {
+    static const int forced = [] {
+      const char* e = std::getenv("MK_GEMM_GM");   // tuning override
+      return e ? std::atoi(e) : 0;
+    }();
+    g.gm = forced > 0 ? forced : 8;
+  }
+  g.gm = std::min<int>(g.gm, grid.y);
   hipLaunchKernelGGL((gemm_kernel<C::BM, C::BN, C::WGM, C::WGN, C::NST, C::OCC, C::LOOP, IN, EPI>), grid, dim3(C::NTH),
                      0, st, g);
 }

@@ -67,6 +67,7 @@ struct GemmArgs {
   const float* aux;           // DQ_SILU_F32A: per-intermediate-channel factor
   int cfg;                    // tile configuration: 0 auto, 1 256x256 (4 waves), 2 256x128, 3 128x128,
                               // 4 256x256 (8 waves)
+  int gm;                     // tile-order group height (rows of tiles); 0 = chosen by the launcher
 };
 int gemm_validate(const GemmArgs& g);
 int launch_gemm(const GemmArgs& g, hipStream_t st);
