@@ -159,6 +159,26 @@ int mk_attn_prefill(const void* qkv, const void* cos, const void* sin, void* out
 int mk_row_quant(const void* x, int x_f32, const float* a, int T, int H, float eps, int norm, int recip,
                  int8_t* q, float* sx, void* stream);
 
+/* Activation quantisation in any of the reference's four activation modes (rows x (T, H) bf16; f32
+ * only for MK_ACT_INT8D), q (T, H) int8 or OCP e4m3 bytes, sx (T,) f32; qmax = 127 (int8) or 448
+ * (fp8):
+ *   dynamic (int8d, fp8d): u = x * a;  s = max(amax|u| * (1/qmax), 1e-6) with MK_ACT_SMUL, else
+ *     max(amax|u| / qmax, 1e-6);  q = u * (1/s) with MK_ACT_RECIP, else u / s;  sx = s * rstd
+ *   static (int8, fp8): t = bf16(x * rstd) with MK_ACT_NORM, else x;  q = t * a;  sx = 1
+ *   int8: q = clip(round_half_even(q), -127, 127);  fp8: q = e4m3_rne(clip(q, -448, 448))
+ *   rstd = rsqrt(mean(x^2) + eps) with MK_ACT_NORM, else 1.
+ * Replaces the activation side of linear / linear_rmsnorm (mk_jax.py:244-299) and the fused prologue
+ * (mk_mlp.py:161-168: MK_ACT_INT8D, NORM | RECIP | SMUL). */
+#define MK_ACT_INT8D 0
+#define MK_ACT_FP8D 1
+#define MK_ACT_INT8 2
+#define MK_ACT_FP8 3
+#define MK_ACT_NORM 1
+#define MK_ACT_RECIP 2
+#define MK_ACT_SMUL 4
+int mk_act_quant(const void* x, int x_f32, const float* a, int T, int H, float eps, int mode, int flags,
+                 void* q, float* sx, void* stream);
+
 /* Epilogues of mk_gemm (C = A(M, K) B(N, K)^T, A and B K-contiguous):                       */
 #define MK_EPI_DQ_BF16 0        /* out bf16 = bf16((acc * rs[m]) * cs[n])        fused_qkv     */
 #define MK_EPI_DQ_SILU 1        /* out bf16 (M, N/2) = silu(g) * u, 32-col g/u interleave       */
@@ -172,9 +192,16 @@ int mk_row_quant(const void* x, int x_f32, const float* a, int T, int H, float e
 #define MK_EPI_I32 9            /* out int32 = acc (int8 operands only)                         */
 #define MK_EPI_SILU_BF16 10     /* out bf16 (M, N/2): g,u = bf16(acc [* (rs[m] * cs[n])]), h = bf16(bf16(silu(g)) * u) */
 #define MK_EPI_DQ2_BF16 11      /* out bf16 = bf16(acc * (rs[m] * cs[n]))         linear_rmsnorm int8d */
+#define MK_EPI_DQ2_RES_BF16ADD 12 /* res = bf16(res + bf16(acc * (rs[m] * cs[n])))  fp8 O / down  */
 
-/* int8 x int8 -> int32 (is_int8 = 1) or bf16 x bf16 -> f32 MFMA GEMM with a fused epilogue. */
-int mk_gemm(int is_int8, int epi, const void* A, int lda, const void* B, int ldb, int M, int N, int K,
+/* Operand types of mk_gemm: int8 x int8 -> int32, bf16 x bf16 -> f32, e4m3 x e4m3 -> f32 (fp8 takes
+ * F32, DQ_BF16, DQ2_BF16, DQ_RES_BF16ADD, DQ2_RES_BF16ADD and SILU_BF16; DQ2_RES_BF16ADD needs
+ * int8 or fp8). */
+#define MK_IN_BF16 0
+#define MK_IN_INT8 1
+#define MK_IN_FP8 2
+/* MFMA GEMM with a fused epilogue; in_type is MK_IN_*. */
+int mk_gemm(int in_type, int epi, const void* A, int lda, const void* B, int ldb, int M, int N, int K,
             void* out, int ldo, void* res, int ldr, const float* rs, const float* cs, const float* aux,
             void* stream);
 
@@ -197,7 +224,7 @@ int mk_bench_attn(const void* qkv, const void* cos, const void* sin, void* out, 
                   int B, int S, int n_q, int n_kv, int head_dim, float sm_scale, int iters, void* stream,
                   float* avg_ms);
 /* One mk_gemm configuration (same arguments as mk_gemm). */
-int mk_bench_gemm(int is_int8, int epi, const void* A, int lda, const void* B, int ldb, int M, int N, int K,
+int mk_bench_gemm(int in_type, int epi, const void* A, int lda, const void* B, int ldb, int M, int N, int K,
                   void* out, int ldo, void* res, int ldr, const float* rs, const float* cs, const float* aux,
                   int iters, void* stream, float* avg_ms);
 

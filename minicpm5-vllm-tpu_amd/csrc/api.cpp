@@ -186,30 +186,44 @@ int mk_bench_attn(const void* qkv, const void* cos, const void* sin, void* out, 
   return time_launches([&] { return mk::launch_attn_stages(a, st, 2); }, iters, st, avg_ms);
 }
 
-int mk_bench_gemm(int is_int8, int epi, const void* A, int lda, const void* B, int ldb, int M, int N, int K,
+int mk_bench_gemm(int in_type, int epi, const void* A, int lda, const void* B, int ldb, int M, int N, int K,
                   void* out, int ldo, void* res, int ldr, const float* rs, const float* cs, const float* aux,
                   int iters, void* stream, float* avg_ms) {
   return time_launches(
-      [&] { return mk_gemm(is_int8, epi, A, lda, B, ldb, M, N, K, out, ldo, res, ldr, rs, cs, aux, stream); }, iters,
+      [&] { return mk_gemm(in_type, epi, A, lda, B, ldb, M, N, K, out, ldo, res, ldr, rs, cs, aux, stream); }, iters,
       static_cast<hipStream_t>(stream), avg_ms);
 }
 
 int mk_row_quant(const void* x, int x_f32, const float* a, int T, int H, float eps, int norm, int recip,
                  int8_t* q, float* sx, void* stream) {
   mk::QuantArgs qa{x, H, x_f32 != 0, a, T, H, eps, norm != 0, recip != 0, q, H, sx};
+  qa.smul = recip != 0;   // the fused prologue computes s = amax * (1/127)
   MK_TRY(mk::launch_rowquant(qa, static_cast<hipStream_t>(stream)));
 }
 
-int mk_gemm(int is_int8, int epi, const void* A, int lda, const void* B, int ldb, int M, int N, int K,
+int mk_act_quant(const void* x, int x_f32, const float* a, int T, int H, float eps, int mode, int flags,
+                 void* q, float* sx, void* stream) {
+  MK_REQUIRE(mode >= MK_ACT_INT8D && mode <= MK_ACT_FP8, "act_quant: unknown mode");
+  MK_REQUIRE((flags & ~(MK_ACT_NORM | MK_ACT_RECIP | MK_ACT_SMUL)) == 0, "act_quant: unknown flags");
+  static const mk::QKind kinds[] = {mk::QKind::I8D, mk::QKind::F8D, mk::QKind::I8S, mk::QKind::F8S};
+  mk::QuantArgs qa{x, H, x_f32 != 0, a, T, H, eps, (flags & MK_ACT_NORM) != 0, (flags & MK_ACT_RECIP) != 0, q, H, sx};
+  qa.kind = kinds[mode];
+  qa.smul = (flags & MK_ACT_SMUL) != 0;
+  MK_TRY(mk::launch_rowquant(qa, static_cast<hipStream_t>(stream)));
+}
+
+int mk_gemm(int in_type, int epi, const void* A, int lda, const void* B, int ldb, int M, int N, int K,
             void* out, int ldo, void* res, int ldr, const float* rs, const float* cs, const float* aux,
             void* stream) {
-  MK_REQUIRE(epi >= MK_EPI_DQ_BF16 && epi <= MK_EPI_DQ2_BF16, "gemm: unknown epilogue");
+  MK_REQUIRE(epi >= MK_EPI_DQ_BF16 && epi <= MK_EPI_DQ2_RES_BF16ADD, "gemm: unknown epilogue");
+  MK_REQUIRE(in_type >= MK_IN_BF16 && in_type <= MK_IN_FP8, "gemm: unknown operand type");
   static const mk::Epi map[] = {mk::Epi::DQ_BF16,        mk::Epi::DQ_SILU,    mk::Epi::DQ_SILU_F32A,
                                 mk::Epi::BF16,           mk::Epi::F32,        mk::Epi::RES_BF16ADD,
                                 mk::Epi::DQ_RES_BF16ADD, mk::Epi::RES_F32ADD, mk::Epi::DQ2_RES_F32ADD,
-                                mk::Epi::I32,            mk::Epi::SILU_BF16,  mk::Epi::DQ2_BF16};
+                                mk::Epi::I32,            mk::Epi::SILU_BF16,  mk::Epi::DQ2_BF16,
+                                mk::Epi::DQ2_RES_BF16ADD};
   mk::GemmArgs g{};
-  g.in = is_int8 ? mk::GemmIn::I8 : mk::GemmIn::BF16;
+  g.in = in_type == MK_IN_INT8 ? mk::GemmIn::I8 : in_type == MK_IN_FP8 ? mk::GemmIn::F8 : mk::GemmIn::BF16;
   g.epi = map[epi];
   g.A = A;
   g.lda = lda;

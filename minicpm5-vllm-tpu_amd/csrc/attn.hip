@@ -413,9 +413,9 @@ int launch_attn_hd(const AttnArgs& a, hipStream_t st, int stages) {
 }
 
 // ---- last-token attention (mk_jax.py:492-520): one query per sequence against all S keys.
-// Kernel 1: workgroup = (256-key chunk, kv head, sequence); thread = key.  Writes per (head,
-// chunk) the partial max m, sum l = sum exp(s - m) and o = sum exp(s - m) v.  Kernel 2 merges the
-// chunks.  RoPE (position S-1 for q, the key's position for k) is computed in f32 and rounded to
+// Kernel 1: workgroup = (256-key chunk, kv head, sequence); thread = key; the last chunk may be
+// partial (S a multiple of 64).  Writes per (head, chunk) the partial max m, sum l = sum exp(s - m)
+// and o = sum exp(s - m) v.  Kernel 2 merges the chunks.  RoPE (position S-1 for q, the key's position for k) is computed in f32 and rounded to
 // bf16, as apply_rope_4d returns bf16 (mk_jax.py:48-52); scores and softmax are f32.
 constexpr int LCH = 256;
 
@@ -425,7 +425,8 @@ __global__ __launch_bounds__(LCH) void last_attn_part_kernel(LastAttnArgs a) {
   __shared__ float ps[G][LCH];
   __shared__ float red[G][LCH / 64];
   const int chunk = blockIdx.x, kv = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
-  const int nchunk = a.S / LCH;
+  const int nchunk = (a.S + LCH - 1) / LCH;
+  const int nkey = min(LCH, a.S - chunk * LCH);   // keys of this chunk (>= 64)
   constexpr int H2 = HD / 2;
   const size_t pos_last = (size_t)(a.S - 1) * HD;
   for (int i = tid; i < G * HD; i += LCH) {
@@ -436,13 +437,14 @@ __global__ __launch_bounds__(LCH) void last_attn_part_kernel(LastAttnArgs a) {
     qs[h][d] = bf2f(f2bf(x * bf2f(a.cos[pos_last + d]) + y * bf2f(a.sin[pos_last + d])));
   }
   __syncthreads();
-  const int t = chunk * LCH + tid;
+  const bool valid = tid < nkey;
+  const int t = chunk * LCH + (valid ? tid : 0);
   const int kvdim = a.n_kv * HD;
   const uint16_t* krow = a.kv + ((size_t)b * a.S + t) * (2 * kvdim) + kv * HD;
   float s[G];
 #pragma unroll
   for (int h = 0; h < G; ++h) s[h] = 0.f;
-  for (int d = 0; d < H2; ++d) {
+  for (int d = 0; d < H2 && valid; ++d) {
     const float x1 = bf2f(krow[d]), x2 = bf2f(krow[d + H2]);
     const size_t tb = (size_t)t * HD;
     const float k1 = bf2f(f2bf(x1 * bf2f(a.cos[tb + d]) - x2 * bf2f(a.sin[tb + d])));
@@ -450,7 +452,11 @@ __global__ __launch_bounds__(LCH) void last_attn_part_kernel(LastAttnArgs a) {
 #pragma unroll
     for (int h = 0; h < G; ++h) s[h] += qs[h][d] * k1 + qs[h][d + H2] * k2;
   }
-  // block max per head
+  if (!valid) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) s[h] = -INFINITY;
+  }
+  // block max per head (finite: every chunk holds at least one key)
   const int lane = tid & 63, w = tid >> 6;
 #pragma unroll
   for (int h = 0; h < G; ++h) {
@@ -480,7 +486,7 @@ __global__ __launch_bounds__(LCH) void last_attn_part_kernel(LastAttnArgs a) {
   for (int i = tid; i < G * HD; i += LCH) {
     const int h = i / HD, d = i % HD;
     float o = 0.f;
-    for (int k = 0; k < LCH; ++k) o += ps[h][k] * bf2f(vbase[(size_t)k * 2 * kvdim + d]);
+    for (int k = 0; k < nkey; ++k) o += ps[h][k] * bf2f(vbase[(size_t)k * 2 * kvdim + d]);
     float* pp = a.part + (((size_t)b * a.n_q + kv * G + h) * nchunk + chunk) * (HD + 2);
     pp[2 + d] = o;
     if (d == 0) {
@@ -495,7 +501,7 @@ __global__ __launch_bounds__(LCH) void last_attn_part_kernel(LastAttnArgs a) {
 template <int HD>
 __global__ void last_attn_merge_kernel(LastAttnArgs a) {
   const int head = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
-  const int nchunk = a.S / LCH;
+  const int nchunk = (a.S + LCH - 1) / LCH;
   const float* pp = a.part + ((size_t)b * a.n_q + head) * nchunk * (HD + 2);
   float M = -INFINITY;
   for (int c = 0; c < nchunk; ++c) M = fmaxf(M, pp[(size_t)c * (HD + 2)]);
@@ -510,7 +516,7 @@ __global__ void last_attn_merge_kernel(LastAttnArgs a) {
 
 template <int HD>
 int launch_last_attn_hd(const LastAttnArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL(last_attn_part_kernel<HD>, dim3(a.S / LCH, a.n_kv, a.B), dim3(LCH), 0, st, a);
+  hipLaunchKernelGGL(last_attn_part_kernel<HD>, dim3((a.S + LCH - 1) / LCH, a.n_kv, a.B), dim3(LCH), 0, st, a);
   MK_HIP_CHECK(hipGetLastError());
   hipLaunchKernelGGL(last_attn_merge_kernel<HD>, dim3(a.n_q, a.B), dim3(HD), 0, st, a);
   MK_HIP_CHECK(hipGetLastError());
@@ -545,13 +551,12 @@ int launch_attn_stages(const AttnArgs& a, hipStream_t st, int stages) {
 int launch_attn(const AttnArgs& a, hipStream_t st) { return launch_attn_stages(a, st, 3); }
 
 size_t last_attn_scratch_bytes(int B, int S, int n_q, int hd) {
-  return (size_t)B * n_q * (S / LCH) * (hd + 2) * sizeof(float);
+  return (size_t)B * n_q * ((S + LCH - 1) / LCH) * (hd + 2) * sizeof(float);
 }
 
 int launch_last_attn(const LastAttnArgs& a, hipStream_t st) {
   int rc = attn_validate(a.B, a.S, a.n_q, a.n_kv, a.hd);
   if (rc) return rc;
-  MK_REQUIRE(a.S % LCH == 0, "last-token attention: seq must be a multiple of 256");
   switch (a.hd) {
     case 64: return launch_last_attn_hd<64>(a, st);
     case 96: return launch_last_attn_hd<96>(a, st);

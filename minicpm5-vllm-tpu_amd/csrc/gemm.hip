@@ -4,8 +4,9 @@
 // (in, out) (mk_weights.py:147-153); the model runner repacks them once to (out, in) so that every
 // lane of a 32x32 MFMA reads 16 contiguous bytes of K for its row / column.
 //
-// int8 (v_mfma_i32_32x32x32_i8, exact int32 accumulation) and bf16 (v_mfma_f32_32x32x16_bf16,
-// f32 accumulation) share one kernel: both consume 16 bytes of K per lane per instruction.
+// int8 (v_mfma_i32_32x32x32_i8, exact int32 accumulation), bf16 (v_mfma_f32_32x32x16_bf16, f32
+// accumulation) and fp8 e4m3 (two v_mfma_f32_32x32x16_fp8_fp8, f32 accumulation) share one kernel:
+// each consumes 16 bytes of K per lane per k-step.
 //
 // Epilogues restate the reference's dequant / activation / residual algebra exactly:
 //   fused_qkv      mk_mlp.py:169-170   out = bf16((acc * sx) * s_w)
@@ -14,6 +15,7 @@
 //                  mk_mlp.py:95-96     out = bf16(x + acc * (s_h * s_d))   (int8 W_down)
 //   linear         mk_jax.py:243,265   bf16(acc) / bf16((acc * s_x) * s_w), then bf16 residual
 //                                      add x + o (mk_jax.py:394)
+//                  mk_jax.py:250,256   fp8: bf16(acc * (s_x * s_w)) / bf16(acc * s_w)
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
@@ -65,6 +67,15 @@ struct Mma<GemmIn::I8> {
   __device__ static float f(int v) { return static_cast<float>(v); }
 };
 template <>
+struct Mma<GemmIn::F8> {
+  using Acc = f32x16;
+  using Elem = float;
+  using Vec4 = f32x4;
+  static constexpr int ESZ = 1;
+  __device__ static Acc run(const u32x4& a, const u32x4& b, const Acc& c) { return mfma_fp8_32x32x32(a, b, c); }
+  __device__ static float f(float v) { return v; }
+};
+template <>
 struct Mma<GemmIn::BF16> {
   using Acc = f32x16;
   using Elem = float;
@@ -96,6 +107,9 @@ __device__ inline void epi_store(const GemmArgs& g, int m, int n, float v) {
   } else if constexpr (EPI == Epi::DQ_RES_BF16ADD) {
     uint16_t* r = g.res + (size_t)m * g.ldr + n;
     *r = f2bf(bf2f(*r) + bf2f(f2bf((v * g.rs[m]) * g.cs[n])));
+  } else if constexpr (EPI == Epi::DQ2_RES_BF16ADD) {
+    uint16_t* r = g.res + (size_t)m * g.ldr + n;
+    *r = f2bf(bf2f(*r) + bf2f(f2bf(v * (g.rs[m] * g.cs[n]))));
   } else if constexpr (EPI == Epi::RES_F32ADD) {
     uint16_t* r = g.res + (size_t)m * g.ldr + n;
     *r = f2bf(bf2f(*r) + v);
@@ -216,10 +230,10 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
   // a 32-row slice and a fixed group of 8 columns (8 gate + 8 up columns for the SiLU epilogues).
   constexpr bool SILU = EPI == Epi::DQ_SILU || EPI == Epi::DQ_SILU_F32A || EPI == Epi::SILU_BF16;
   constexpr bool RES = EPI == Epi::RES_BF16ADD || EPI == Epi::DQ_RES_BF16ADD || EPI == Epi::RES_F32ADD ||
-                       EPI == Epi::DQ2_RES_F32ADD;
+                       EPI == Epi::DQ2_RES_F32ADD || EPI == Epi::DQ2_RES_BF16ADD;
   constexpr bool DQ = EPI == Epi::DQ_BF16 || EPI == Epi::DQ2_BF16 || EPI == Epi::DQ_RES_BF16ADD ||
-                      EPI == Epi::DQ2_RES_F32ADD || EPI == Epi::DQ_SILU || EPI == Epi::DQ_SILU_F32A ||
-                      EPI == Epi::SILU_BF16;    // SILU_BF16: only when scales are given
+                      EPI == Epi::DQ2_RES_F32ADD || EPI == Epi::DQ2_RES_BF16ADD || EPI == Epi::DQ_SILU ||
+                      EPI == Epi::DQ_SILU_F32A || EPI == Epi::SILU_BF16;   // SILU_BF16: only with scales
   constexpr int TPR = SILU ? C::WN / 16 : C::WN / 8;   // tasks per row
   constexpr int TRS = 64 / TPR;                        // rows between a lane's tasks
   constexpr int NTASK = 32 / TRS;
@@ -491,7 +505,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
             const float cs = csv[e >> 2][e & 3];
-            if constexpr (EPI == Epi::DQ2_BF16 || EPI == Epi::DQ2_RES_F32ADD) v[e] = v[e] * (rsv[mt][i] * cs);
+            if constexpr (EPI == Epi::DQ2_BF16 || EPI == Epi::DQ2_RES_F32ADD || EPI == Epi::DQ2_RES_BF16ADD)
+              v[e] = v[e] * (rsv[mt][i] * cs);
             else v[e] = (v[e] * rsv[mt][i]) * cs;
           }
         }
@@ -501,7 +516,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
           float a = v[2 * e], b = v[2 * e + 1];
           if constexpr (RES) {
             const float ra = bf_lo(rv[mt & 1][i][e]), rb = bf_hi(rv[mt & 1][i][e]);
-            if constexpr (EPI == Epi::RES_BF16ADD || EPI == Epi::DQ_RES_BF16ADD) {
+            if constexpr (EPI == Epi::RES_BF16ADD || EPI == Epi::DQ_RES_BF16ADD || EPI == Epi::DQ2_RES_BF16ADD) {
               a = ra + bf2f(f2bf(a));
               b = rb + bf2f(f2bf(b));
             } else {
@@ -626,13 +641,43 @@ void launch_skinny_t(const GemmArgs& g, hipStream_t st) {
   hipLaunchKernelGGL((gemm_skinny_kernel<IN, EPI>), grid, dim3(64 * SK_WAVES), 0, st, g);
 }
 
+// Epilogues built per operand type: fp8 operands only come with the dequantising epilogues of the
+// fp8 / fp8d linears (and F32 for tests); the bf16 GEMMs never dequantise a residual in bf16.
+template <GemmIn IN>
+constexpr bool epi_built(Epi e) {
+  if constexpr (IN == GemmIn::F8)
+    return e == Epi::F32 || e == Epi::DQ_BF16 || e == Epi::DQ2_BF16 || e == Epi::DQ_RES_BF16ADD ||
+           e == Epi::DQ2_RES_BF16ADD || e == Epi::SILU_BF16;
+  if constexpr (IN == GemmIn::BF16) return e != Epi::I32 && e != Epi::DQ2_RES_BF16ADD;
+  return true;
+}
+
+template <GemmIn IN, Epi E>
+int launch_e(const GemmArgs& g, hipStream_t st, bool skinny) {
+  if constexpr (!epi_built<IN>(E)) {
+    set_error("gemm: epilogue not built for this operand type");
+    return MK_EUNSUPPORTED;
+  } else {
+    constexpr bool silu = E == Epi::SILU_BF16 || E == Epi::DQ_SILU || E == Epi::DQ_SILU_F32A;
+    if constexpr (silu) {
+      if (skinny) {
+        set_error("gemm: the SiLU epilogues have no skinny variant");
+        return MK_EUNSUPPORTED;
+      }
+      launch_t<IN, E>(g, st);
+    } else {
+      if (skinny) launch_skinny_t<IN, E>(g, st);
+      else launch_t<IN, E>(g, st);
+    }
+    MK_HIP_CHECK(hipGetLastError());
+    return MK_OK;
+  }
+}
+
 template <GemmIn IN>
 int dispatch(const GemmArgs& g, hipStream_t st, bool skinny) {
-#define MK_CASE(E)                                          \
-  case Epi::E:                                              \
-    if (skinny) launch_skinny_t<IN, Epi::E>(g, st);         \
-    else launch_t<IN, Epi::E>(g, st);                       \
-    break;
+#define MK_CASE(E) \
+  case Epi::E: return launch_e<IN, Epi::E>(g, st, skinny);
   switch (g.epi) {
     MK_CASE(DQ_BF16)
     MK_CASE(BF16)
@@ -643,28 +688,20 @@ int dispatch(const GemmArgs& g, hipStream_t st, bool skinny) {
     MK_CASE(DQ2_RES_F32ADD)
     MK_CASE(I32)
     MK_CASE(DQ2_BF16)
-    case Epi::SILU_BF16:
-      if (skinny) { set_error("gemm: SILU_BF16 has no skinny variant"); return MK_EUNSUPPORTED; }
-      launch_t<IN, Epi::SILU_BF16>(g, st);
-      break;
-    case Epi::DQ_SILU:
-      if (skinny) { set_error("gemm: DQ_SILU has no skinny variant"); return MK_EUNSUPPORTED; }
-      launch_t<IN, Epi::DQ_SILU>(g, st);
-      break;
-    case Epi::DQ_SILU_F32A:
-      if (skinny) { set_error("gemm: DQ_SILU_F32A has no skinny variant"); return MK_EUNSUPPORTED; }
-      launch_t<IN, Epi::DQ_SILU_F32A>(g, st);
-      break;
+    MK_CASE(DQ2_RES_BF16ADD)
+    MK_CASE(SILU_BF16)
+    MK_CASE(DQ_SILU)
+    MK_CASE(DQ_SILU_F32A)
   }
 #undef MK_CASE
-  MK_HIP_CHECK(hipGetLastError());
-  return MK_OK;
+  set_error("gemm: unknown epilogue");
+  return MK_EINVAL;
 }
 
 }  // namespace
 
 int gemm_validate(const GemmArgs& g) {
-  const int esz = g.in == GemmIn::I8 ? 1 : 2;
+  const int esz = g.in == GemmIn::BF16 ? 2 : 1;
   MK_REQUIRE(g.A && g.B, "gemm: null operand");
   MK_REQUIRE(g.M >= 1 && g.N >= 1 && g.K >= 1, "gemm: empty problem");
   MK_REQUIRE((g.K * esz) % 32 == 0, "gemm: K bytes must be a multiple of 32");
@@ -672,10 +709,11 @@ int gemm_validate(const GemmArgs& g) {
              "gemm: operand strides must be >= K and 16-byte aligned");
   MK_REQUIRE(((uintptr_t)g.A % 16) == 0 && ((uintptr_t)g.B % 16) == 0, "gemm: operands must be 16-byte aligned");
   const bool res = g.epi == Epi::RES_BF16ADD || g.epi == Epi::DQ_RES_BF16ADD || g.epi == Epi::RES_F32ADD ||
-                   g.epi == Epi::DQ2_RES_F32ADD;
+                   g.epi == Epi::DQ2_RES_F32ADD || g.epi == Epi::DQ2_RES_BF16ADD;
   MK_REQUIRE(res ? (g.res != nullptr && g.ldr >= g.N) : (g.out != nullptr && g.ldo >= 1), "gemm: missing output");
   const bool dq = g.epi == Epi::DQ_BF16 || g.epi == Epi::DQ_SILU || g.epi == Epi::DQ_SILU_F32A ||
-                  g.epi == Epi::DQ_RES_BF16ADD || g.epi == Epi::DQ2_RES_F32ADD || g.epi == Epi::DQ2_BF16;
+                  g.epi == Epi::DQ_RES_BF16ADD || g.epi == Epi::DQ2_RES_F32ADD || g.epi == Epi::DQ2_BF16 ||
+                  g.epi == Epi::DQ2_RES_BF16ADD;
   MK_REQUIRE(!dq || (g.rs && g.cs), "gemm: dequant epilogue needs row and column scales");
   MK_REQUIRE(g.epi != Epi::SILU_BF16 || (!g.rs == !g.cs), "gemm: SILU_BF16 takes both scales or neither");
   MK_REQUIRE(g.epi != Epi::I32 || g.in == GemmIn::I8, "gemm: the I32 epilogue needs int8 operands");
@@ -689,10 +727,10 @@ int gemm_validate(const GemmArgs& g) {
 int launch_gemm(const GemmArgs& g, hipStream_t st) {
   int rc = gemm_validate(g);
   if (rc) return rc;
-  MK_REQUIRE((g.K * (g.in == GemmIn::I8 ? 1 : 2)) % BKB == 0, "gemm: K bytes must be a multiple of 64");
+  MK_REQUIRE((g.K * (g.in == GemmIn::BF16 ? 2 : 1)) % BKB == 0, "gemm: K bytes must be a multiple of 64");
   MK_REQUIRE(g.N % 8 == 0 && (g.ldo % 8 == 0) && (g.ldr % 8 == 0), "gemm: N and output strides must be multiples of 8");
   {
-    const uint64_t esz = g.in == GemmIn::I8 ? 1 : 2;
+    const uint64_t esz = g.in == GemmIn::BF16 ? 2 : 1;
     MK_REQUIRE((uint64_t)(g.M - 1) * g.lda * esz + g.K * esz < (1ull << 32) &&
                    (uint64_t)(g.N - 1) * g.ldb * esz + g.K * esz < (1ull << 32),
                "gemm: each operand must span less than 4 GiB");
@@ -700,14 +738,22 @@ int launch_gemm(const GemmArgs& g, hipStream_t st) {
   MK_REQUIRE(((uintptr_t)g.out % 16) == 0 && ((uintptr_t)g.res % 16) == 0 && ((uintptr_t)g.cs % 16) == 0 &&
                  ((uintptr_t)g.aux % 16) == 0,
              "gemm: output, residual and scale vectors must be 16-byte aligned");
-  return g.in == GemmIn::I8 ? dispatch<GemmIn::I8>(g, st, false) : dispatch<GemmIn::BF16>(g, st, false);
+  switch (g.in) {
+    case GemmIn::I8: return dispatch<GemmIn::I8>(g, st, false);
+    case GemmIn::F8: return dispatch<GemmIn::F8>(g, st, false);
+    default: return dispatch<GemmIn::BF16>(g, st, false);
+  }
 }
 
 int launch_gemm_skinny(const GemmArgs& g, hipStream_t st) {
   int rc = gemm_validate(g);
   if (rc) return rc;
   MK_REQUIRE(g.M <= 32, "gemm_skinny: M must be <= 32");
-  return g.in == GemmIn::I8 ? dispatch<GemmIn::I8>(g, st, true) : dispatch<GemmIn::BF16>(g, st, true);
+  switch (g.in) {
+    case GemmIn::I8: return dispatch<GemmIn::I8>(g, st, true);
+    case GemmIn::F8: return dispatch<GemmIn::F8>(g, st, true);
+    default: return dispatch<GemmIn::BF16>(g, st, true);
+  }
 }
 
 }  // namespace mk

@@ -39,7 +39,7 @@ int launch_last_attn(const LastAttnArgs& a, hipStream_t st);
 
 // ------------------------------------------------------------------------------ GEMM
 // C(M, N) = A(M, K) * B(N, K)^T with A and B K-contiguous (row stride lda / ldb elements).
-enum class GemmIn { I8, BF16 };
+enum class GemmIn { I8, BF16, F8 };   // F8: OCP e4m3 operands, f32 accumulation
 enum class Epi {
   DQ_BF16,        // out = bf16((acc * rs[m]) * cs[n])                      (fused_qkv)
   DQ_SILU,        // g/u interleaved by 32 columns: h = silu(g) * u, g,u = (acc * rs[m]) * cs[n]
@@ -53,6 +53,7 @@ enum class Epi {
   I32,            // out = acc (int32, raw accumulator; tests)
   SILU_BF16,      // g/u interleaved: g, u = bf16(acc [* (rs[m] * cs[n])]); h = bf16(bf16(silu(g)) * u)
   DQ2_BF16,       // out = bf16(acc * (rs[m] * cs[n]))                     (linear_rmsnorm int8d)
+  DQ2_RES_BF16ADD,// res = bf16(res + bf16(acc * (rs[m] * cs[n])))          (fp8d O / down projection)
 };
 struct GemmArgs {
   GemmIn in;
@@ -76,18 +77,25 @@ int launch_gemm(const GemmArgs& g, hipStream_t st);
 int launch_gemm_skinny(const GemmArgs& g, hipStream_t st);
 
 // ------------------------------------------------------------------------------ norm / quant
-// Fused RMSNorm statistics + per-token dynamic int8 quantisation (mk_mlp.py:161-168):
-//   rstd = rsqrt(mean(x^2) + eps); u = x * a; s_u = max(amax|u| / 127, 1e-6);
-//   q = round_half_even(u / s_u); sx = s_u * rstd.   `recip` selects u * (1/s_u) (fused kernels)
-//   instead of u / s_u (XLA path).  With norm == false, rstd is 1 (plain dynamic quant, linear()).
+// Activation quantisation of rows x (T, H), one kernel for the reference's four activation modes
+// (qmax = 127 for int8, 448 for fp8 e4m3; rstd = rsqrt(mean(x^2) + eps) with norm, else 1):
+//   dynamic (int8d, fp8d; mk_mlp.py:161-168, mk_jax.py:244-262, :283-297):
+//     u = x * a;  s = max(amax|u| * (1/qmax), 1e-6) (smul) or max(amax|u| / qmax, 1e-6);
+//     q = u * (1/s) (recip) or u / s;  sx = s * rstd
+//   static (int8, fp8; mk_jax.py:252-256, :265-268, linear_rmsnorm's fallback :298-299):
+//     t = norm ? bf16(x * rstd) : x;  q = t * a;  sx = 1
+//   int8: q = clip(round_half_even(q), -127, 127);  fp8: q = e4m3(clip(q, -448, 448)).
+enum class QKind { I8D, F8D, I8S, F8S };
 struct QuantArgs {
   const void* x; int ldx; bool x_f32;
   const float* a;        // per-channel factor or null (ones)
   int T, H;
   float eps;
   bool norm, recip;
-  int8_t* q; int ldq;
+  void* q; int ldq;      // int8 or e4m3 bytes
   float* sx;
+  QKind kind = QKind::I8D;
+  bool smul = false;
 };
 int launch_rowquant(const QuantArgs& a, hipStream_t st);
 

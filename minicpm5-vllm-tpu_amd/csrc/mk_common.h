@@ -69,6 +69,23 @@ __device__ inline i32x16 mfma_i8_32x32x32(const u32x4& a, const u32x4& b, const 
   return __builtin_amdgcn_mfma_i32_32x32x32_i8(bitcast<i32x4>(a), bitcast<i32x4>(b), c, 0, 0, 0);
 }
 
+// fp8 (OCP e4m3 on gfx950) operands: two v_mfma_f32_32x32x16_fp8_fp8 over the 16 bytes of K a lane
+// holds (bytes 0-7, then 8-15); f32 accumulation.
+typedef long i64x2 __attribute__((ext_vector_type(2)));
+__device__ inline f32x16 mfma_fp8_32x32x32(const u32x4& a, const u32x4& b, const f32x16& c) {
+  const i64x2 a2 = bitcast<i64x2>(a), b2 = bitcast<i64x2>(b);
+  const f32x16 t = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(a2[0], b2[0], c, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(a2[1], b2[1], t, 0, 0, 0);
+}
+
+// f32 -> OCP e4m3 (float8_e4m3fn) with round-to-nearest-even (v_cvt_pk_fp8_f32).  Callers clip to
+// [-448, 448] first, as the reference does before its cast, so no value saturates.
+__device__ inline uint32_t pack_fp8x4(float a, float b, float c, float d) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+  return static_cast<uint32_t>(w);
+}
+
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // acc + lo(w) + hi(w) for a packed bf16 pair (v_dot2_f32_bf16 with (1, 1))

@@ -33,6 +33,34 @@ int mlp_chunk(int I) {
   return I;
 }
 
+// Activation quantisation of a quantised linear's input on the reference's unfused (XLA) path:
+//   linear_rmsnorm (norm, mk_jax.py:272-299): dynamic s = amax * (1/qmax), q = u / s; static modes
+//     round x * rstd to bf16 first;
+//   linear (mk_jax.py:244-268): int8d s = amax / 127, q = u / s; fp8d s = amax * (1/448), q = u * (1/s);
+//   the down projection quantises dynamically in the static modes too (dynamic_act, mk_jax.py:422-423).
+QuantArgs act_quant(LinQ mode, bool norm, bool down, const void* x, int ldx, const float* a, int T, int H,
+                    float eps, void* q, float* sx) {
+  QuantArgs qa{x, ldx, false, a, T, H, eps, norm, false, q, H, sx};
+  if (down && mode == LQ_I8S) mode = LQ_I8D;
+  if (down && mode == LQ_F8S) mode = LQ_F8D;
+  switch (mode) {
+    case LQ_I8S: qa.kind = QKind::I8S; break;
+    case LQ_F8S: qa.kind = QKind::F8S; break;
+    case LQ_F8D:
+      qa.kind = QKind::F8D;
+      qa.smul = true;
+      qa.recip = !norm;
+      break;
+    default:
+      qa.kind = QKind::I8D;
+      qa.smul = norm;
+      break;
+  }
+  return qa;
+}
+
+inline bool fp8(LinQ m) { return m == LQ_F8D || m == LQ_F8S; }
+
 }  // namespace
 
 int parse_quant(const char* quant, QuantPlan* p) {
@@ -55,14 +83,14 @@ int parse_quant(const char* quant, QuantPlan* p) {
     q = base.substr(0, colon);
     lins = base.substr(colon + 1);
   }
-  if (q == "int8" || q == "fp8" || q == "fp8d") {
-    set_error("quant '" + q + "' (static int8 / fp8 activations) is not built for MI355X yet");
-    return MK_EUNSUPPORTED;
-  }
-  MK_REQUIRE(q == "bf16" || q == "int8d", "quant: unknown base '" + q + "' (bf16 | int8d)");
-  const bool qi8 = q == "int8d";
+  LinQ lq = LQ_BF16;
+  if (q == "int8d") lq = LQ_I8D;
+  else if (q == "int8") lq = LQ_I8S;
+  else if (q == "fp8d") lq = LQ_F8D;
+  else if (q == "fp8") lq = LQ_F8S;
+  else MK_REQUIRE(q == "bf16", "quant: unknown base '" + q + "' (bf16 | int8 | int8d | fp8 | fp8d)");
   const char* names[4] = {"qkv", "o", "gu", "down"};
-  for (int i = 0; i < 4; ++i) p->i8[i] = all ? qi8 : false;
+  for (int i = 0; i < 4; ++i) p->mode[i] = all ? lq : LQ_BF16;
   if (!all) {
     size_t a = 0;
     while (a <= lins.size()) {
@@ -72,7 +100,7 @@ int parse_quant(const char* quant, QuantPlan* p) {
       for (int i = 0; i < 4; ++i)
         if (lin == names[i]) k = i;
       MK_REQUIRE(k >= 0, "quant: unknown linear '" + lin + "' (qkv | o | gu | down)");
-      p->i8[k] = qi8;
+      p->mode[k] = lq;
       if (b == std::string::npos) break;
       a = b + 1;
     }
@@ -86,9 +114,12 @@ int parse_quant(const char* quant, QuantPlan* p) {
     else if (f == "fmlp") p->fmlp = true;
     else MK_REQUIRE(false, "quant: unknown flag '" + f + "' (sq | lastbf16 | fqkv | fmlp)");
   }
-  // effective flags: fused kernels only exist for int8 inputs (mk_jax.py:400-403, mk_weights.py:255)
-  p->fqkv = p->fqkv && p->i8[0];
-  p->fmlp = p->fmlp && p->i8[2];
+  for (int i = 0; i < 4; ++i) p->i8[i] = p->mode[i] != LQ_BF16;
+  // effective flags: the fused QKV kernel only for int8d (mk_jax.py:400-403); the fused MLP whenever
+  // W_gu is int8 (int8 or int8d), whose weights are then interleaved (mk_weights.py:255-258) -- its
+  // activations are per-token dynamic either way (mk_mlp.py:68-97)
+  p->fqkv = p->fqkv && p->mode[0] == LQ_I8D;
+  p->fmlp = p->fmlp && (p->mode[2] == LQ_I8D || p->mode[2] == LQ_I8S);
   return MK_OK;
 }
 
@@ -99,7 +130,7 @@ int validate_config(const mk_config* c) {
   MK_REQUIRE(c->inter >= 64 && c->inter % 64 == 0, "config: inter must be a positive multiple of 64");
   MK_REQUIRE(c->vocab >= 1, "config: vocab must be >= 1");
   MK_REQUIRE(c->eps > 0.f, "config: eps must be > 0");
-  MK_REQUIRE(c->max_seq >= 256, "config: max_seq must be >= 256");
+  MK_REQUIRE(c->max_seq >= 128, "config: max_seq must be >= 128");
   int rc = attn_validate(1, 64, c->n_q, c->n_kv, c->head_dim);
   if (rc) return rc;
   return MK_OK;
@@ -332,10 +363,14 @@ int launch_forward(const Fwd& f, hipStream_t st) {
     g.ldo = D;
     g.B = pb + m.P.wqkv + (size_t)l * D * H * e0;
     if (q.i8[0]) {
-      QuantArgs qa{x, H, false, m.w.a_qkv + (size_t)l * H, T, H, c.eps, true, q.fqkv, xq, H, sx};
+      QuantArgs qa = act_quant(q.mode[0], true, false, x, H, m.w.a_qkv + (size_t)l * H, T, H, c.eps, xq, sx);
+      if (q.fqkv) {   // fused_qkv prologue (mk_mlp.py:161-168)
+        qa.recip = true;
+        qa.smul = true;
+      }
       kind = MK_KERNEL_NORM;
       MK_RUN(launch_rowquant(qa, st));
-      g.in = GemmIn::I8;
+      g.in = fp8(q.mode[0]) ? GemmIn::F8 : GemmIn::I8;
       g.A = xq;
       g.rs = sx;
       g.cs = m.w.s_qkv + (size_t)l * D;
@@ -380,14 +415,15 @@ int launch_forward(const Fwd& f, hipStream_t st) {
     go.ldr = H;
     go.B = pb + m.P.wo + (size_t)l * H * qd * e1;
     if (q.i8[1]) {
-      QuantArgs qa{attn, qd, false, m.w.a_o + (size_t)l * qd, T, qd, c.eps, false, false, xq, qd, sx};
+      const QuantArgs qa = act_quant(q.mode[1], false, false, attn, qd, m.w.a_o + (size_t)l * qd, T, qd, c.eps, xq, sx);
       kind = MK_KERNEL_NORM;
       MK_RUN(launch_rowquant(qa, st));
-      go.in = GemmIn::I8;
+      go.in = fp8(q.mode[1]) ? GemmIn::F8 : GemmIn::I8;
       go.A = xq;
       go.rs = sx;
       go.cs = m.w.s_o + (size_t)l * H;
-      go.epi = Epi::DQ_RES_BF16ADD;
+      // int8: bf16((acc * s_x) * s_w) (mk_jax.py:262,268); fp8: bf16(acc * (s_x * s_w)) (:250,256)
+      go.epi = fp8(q.mode[1]) ? Epi::DQ2_RES_BF16ADD : Epi::DQ_RES_BF16ADD;
     } else {
       go.in = GemmIn::BF16;
       go.A = attn;
@@ -407,10 +443,15 @@ int launch_forward(const Fwd& f, hipStream_t st) {
     gu.ldo = I;
     gu.B = pb + m.P.wgu + (size_t)l * 2 * I * H * e2;
     if (q.i8[2]) {
-      QuantArgs qa{x, H, false, m.w.a_gu + (size_t)l * H, T, H, c.eps, true, q.fmlp, xq, H, sx};
+      QuantArgs qa = act_quant(q.mode[2], true, false, x, H, m.w.a_gu + (size_t)l * H, T, H, c.eps, xq, sx);
+      if (q.fmlp) {   // fused_mlp prologue (mk_mlp.py:68-80): dynamic int8, u * (1/s)
+        qa.kind = QKind::I8D;
+        qa.recip = true;
+        qa.smul = true;
+      }
       kind = MK_KERNEL_NORM;
       MK_RUN(launch_rowquant(qa, st));
-      gu.in = GemmIn::I8;
+      gu.in = fp8(q.mode[2]) ? GemmIn::F8 : GemmIn::I8;
       gu.A = xq;
       gu.rs = sx;
       gu.cs = reinterpret_cast<const float*>(pb + m.P.sgu) + (size_t)l * 2 * I;
@@ -437,15 +478,21 @@ int launch_forward(const Fwd& f, hipStream_t st) {
     if (q.i8[3]) {
       // fused int8 down (mk_mlp.py:85-95) quantises h * a_down (already applied) with u * (1/s);
       // the XLA int8d linear quantises h * a_down with u / s (mk_jax.py:257-262)
-      QuantArgs qa{h, I, d8, d8 ? nullptr : m.w.a_down + (size_t)l * I, T, I, c.eps, false, d8, xq, I, sx};
+      QuantArgs qa = act_quant(q.mode[3], false, true, h, I, m.w.a_down + (size_t)l * I, T, I, c.eps, xq, sx);
+      if (d8) {
+        qa.x_f32 = true;
+        qa.a = nullptr;
+        qa.recip = true;
+        qa.smul = true;
+      }
       kind = MK_KERNEL_NORM;
       MK_RUN(launch_rowquant(qa, st));
-      gd.in = GemmIn::I8;
+      gd.in = fp8(q.mode[3]) ? GemmIn::F8 : GemmIn::I8;
       gd.A = xq;
       gd.lda = I;
       gd.rs = sx;
       gd.cs = m.w.s_down + (size_t)l * H;
-      gd.epi = d8 ? Epi::DQ2_RES_F32ADD : Epi::DQ_RES_BF16ADD;
+      gd.epi = d8 ? Epi::DQ2_RES_F32ADD : fp8(q.mode[3]) ? Epi::DQ2_RES_BF16ADD : Epi::DQ_RES_BF16ADD;
     } else {
       gd.in = GemmIn::BF16;
       gd.A = h;
@@ -596,7 +643,7 @@ int launch_forward(const Fwd& f, hipStream_t st) {
 
 int validate_run(const mk_config& c, int bs, int seq) {
   MK_REQUIRE(bs >= 1, "forward: bs must be >= 1");
-  MK_REQUIRE(seq >= 256 && seq % 256 == 0, "forward: seq must be a positive multiple of 256");
+  MK_REQUIRE(seq >= 128 && seq % 128 == 0, "forward: seq must be a positive multiple of 128");
   MK_REQUIRE(seq <= c.max_seq, "forward: seq exceeds the RoPE table rows (max_seq)");
   MK_REQUIRE((long long)bs * seq <= (1LL << 30), "forward: bs * seq too large");
   return MK_OK;

@@ -10,8 +10,11 @@
 namespace mk {
 
 // Per-linear precision + flags of a quant string (mk_jax.py:302-318).
+// Precision of one linear (the quant string's base applied to it, mk_jax.py:302-318).
+enum LinQ : uint8_t { LQ_BF16, LQ_I8D, LQ_I8S, LQ_F8D, LQ_F8S };
 struct QuantPlan {
-  bool i8[4];       // qkv, o, gu, down: int8 weights + per-token dynamic int8 activations
+  LinQ mode[4];     // qkv, o, gu, down
+  bool i8[4];       // 8-bit (int8 or fp8 e4m3) weights
   bool sq, lastbf16, fqkv, fmlp;
 };
 

@@ -33,12 +33,13 @@ __device__ inline void load8(const void* x, size_t off, float v[8]) {
   }
 }
 
-// Reference algebra: mk_mlp.py:161-168 (fused kernels, recip == true) and
-// mk_jax.py:257-262 / :283-286 (XLA linear / linear_rmsnorm, recip == false).
-// One wave per row; the row stays in registers (NC 8-element chunks per lane, all loads issued
-// before the first use) so the row costs one HBM round trip.
-template <bool F32, int NC>
+// Reference algebra: QuantArgs (kernels.h).  One wave per row; the row stays in registers (NC
+// 8-element chunks per lane, all loads issued before the first use) so the row costs one HBM round trip.
+template <bool F32, int NC, QKind KIND>
 __global__ __launch_bounds__(256) void rowquant_kernel(QuantArgs a) {
+  constexpr bool DYN = KIND == QKind::I8D || KIND == QKind::F8D;
+  constexpr bool FP8 = KIND == QKind::F8D || KIND == QKind::F8S;
+  constexpr float QMAX = FP8 ? 448.f : 127.f;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (row >= a.T) return;
   const int nc = a.H / 8;
@@ -49,47 +50,74 @@ __global__ __launch_bounds__(256) void rowquant_kernel(QuantArgs a) {
     const int c = lane + 64 * i;
     if (c < nc) load8<F32>(a.x, xo + 8 * c, v[i]);
   }
+  auto load_a = [&](int c, f32x4& a0, f32x4& a1) {
+    a0 = f32x4{1.f, 1.f, 1.f, 1.f};
+    a1 = a0;
+    if (a.a) {
+      const f32x4* ap = reinterpret_cast<const f32x4*>(a.a + 8 * c);
+      a0 = ap[0];
+      a1 = ap[1];
+    }
+  };
   float ss = 0.f, am = 0.f;
 #pragma unroll
   for (int i = 0; i < NC; ++i) {
     const int c = lane + 64 * i;
     if (c < nc) {
-      f32x4 a0 = {1.f, 1.f, 1.f, 1.f}, a1 = {1.f, 1.f, 1.f, 1.f};
-      if (a.a) {
-        const f32x4* ap = reinterpret_cast<const f32x4*>(a.a + 8 * c);
-        a0 = ap[0];
-        a1 = ap[1];
-      }
+      f32x4 a0, a1;
+      if constexpr (DYN) load_a(c, a0, a1);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         ss += v[i][e] * v[i][e];
-        v[i][e] = a.a ? v[i][e] * (e < 4 ? a0[e] : a1[e - 4]) : v[i][e];   // u = x * a
-        am = fmaxf(am, fabsf(v[i][e]));
+        if constexpr (DYN) {
+          v[i][e] = a.a ? v[i][e] * (e < 4 ? a0[e] : a1[e - 4]) : v[i][e];   // u = x * a
+          am = fmaxf(am, fabsf(v[i][e]));
+        }
       }
     }
   }
   ss = wave_sum(ss);
-  am = wave_max(am);
+  if constexpr (DYN) am = wave_max(am);
   const float rstd = a.norm ? 1.f / sqrtf(ss / (float)a.H + a.eps) : 1.f;
-  const float s_u = a.recip ? fmaxf(am * (1.0f / 127.0f), 1e-6f) : fmaxf(am / 127.0f, 1e-6f);
+  float s_u = 1.f;
+  if constexpr (DYN) s_u = a.smul ? fmaxf(am * (1.0f / QMAX), 1e-6f) : fmaxf(am / QMAX, 1e-6f);
   const float inv = 1.f / s_u;
-  int8_t* qrow = a.q + (size_t)row * a.ldq;
+  uint8_t* qrow = static_cast<uint8_t*>(a.q) + (size_t)row * a.ldq;
 #pragma unroll
   for (int i = 0; i < NC; ++i) {
     const int c = lane + 64 * i;
     if (c >= nc) continue;
-    uint32_t w0 = 0, w1 = 0;
+    float t[8];
+    if constexpr (DYN) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float q = a.recip ? rintf(v[i][e] * inv) : rintf(v[i][e] / s_u);
-      q = fminf(fmaxf(q, -127.f), 127.f);
-      const uint32_t b = static_cast<uint32_t>(static_cast<int32_t>(q)) & 0xffu;
-      if (e < 4) w0 |= b << (8 * e);
-      else w1 |= b << (8 * (e - 4));
+      for (int e = 0; e < 8; ++e) t[e] = a.recip ? v[i][e] * inv : v[i][e] / s_u;
+    } else {
+      f32x4 a0, a1;
+      load_a(c, a0, a1);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float xn = a.norm ? bf2f(f2bf(v[i][e] * rstd)) : v[i][e];
+        t[e] = xn * (e < 4 ? a0[e] : a1[e - 4]);
+      }
+    }
+    uint32_t w0 = 0, w1 = 0;
+    if constexpr (FP8) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) t[e] = fminf(fmaxf(t[e], -448.f), 448.f);
+      w0 = pack_fp8x4(t[0], t[1], t[2], t[3]);
+      w1 = pack_fp8x4(t[4], t[5], t[6], t[7]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float q = fminf(fmaxf(rintf(t[e]), -127.f), 127.f);
+        const uint32_t b = static_cast<uint32_t>(static_cast<int32_t>(q)) & 0xffu;
+        if (e < 4) w0 |= b << (8 * e);
+        else w1 |= b << (8 * (e - 4));
+      }
     }
     *reinterpret_cast<u32x2*>(qrow + 8 * c) = u32x2{w0, w1};
   }
-  if (lane == 0) a.sx[row] = s_u * rstd;
+  if (lane == 0) a.sx[row] = DYN ? s_u * rstd : 1.f;
 }
 
 __global__ __launch_bounds__(256) void rmsnorm_bf16_kernel(const uint16_t* __restrict__ x, int ldx,
@@ -180,9 +208,17 @@ int launch_rowquant(const QuantArgs& a, hipStream_t st) {
              "rowquant: x / a must be 16-byte and q 8-byte aligned");
   const dim3 grid((a.T + 3) / 4);
   const int nc = (a.H / 8 + 63) / 64;   // 8-element chunks per lane
-#define MK_RQ(NC)                                                                                      \
-  if (a.x_f32) hipLaunchKernelGGL((rowquant_kernel<true, NC>), grid, dim3(256), 0, st, a);          \
-  else hipLaunchKernelGGL((rowquant_kernel<false, NC>), grid, dim3(256), 0, st, a);
+  MK_REQUIRE(!a.x_f32 || a.kind == QKind::I8D, "rowquant: f32 input is only taken by the int8d mode");
+#define MK_RQK(NC, K)                                                                                   \
+  if (a.x_f32) hipLaunchKernelGGL((rowquant_kernel<true, NC, K>), grid, dim3(256), 0, st, a);        \
+  else hipLaunchKernelGGL((rowquant_kernel<false, NC, K>), grid, dim3(256), 0, st, a);
+#define MK_RQ(NC)                                                                          \
+  switch (a.kind) {                                                                        \
+    case QKind::I8D: MK_RQK(NC, QKind::I8D) break;                                         \
+    case QKind::F8D: hipLaunchKernelGGL((rowquant_kernel<false, NC, QKind::F8D>), grid, dim3(256), 0, st, a); break; \
+    case QKind::I8S: hipLaunchKernelGGL((rowquant_kernel<false, NC, QKind::I8S>), grid, dim3(256), 0, st, a); break; \
+    case QKind::F8S: hipLaunchKernelGGL((rowquant_kernel<false, NC, QKind::F8S>), grid, dim3(256), 0, st, a); break; \
+  }
   if (nc <= 4) {
     MK_RQ(4)
   } else if (nc <= 8) {
@@ -193,6 +229,7 @@ int launch_rowquant(const QuantArgs& a, hipStream_t st) {
     MK_RQ(16)
   }
 #undef MK_RQ
+#undef MK_RQK
   MK_HIP_CHECK(hipGetLastError());
   return MK_OK;
 }

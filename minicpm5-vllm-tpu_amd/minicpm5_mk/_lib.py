@@ -17,6 +17,7 @@ MK_OK = 0
 EPI = {
     "dq_bf16": 0, "dq_silu": 1, "dq_silu_f32a": 2, "bf16": 3, "f32": 4, "res_bf16add": 5,
     "dq_res_bf16add": 6, "res_f32add": 7, "dq2_res_f32add": 8, "i32": 9, "silu_bf16": 10, "dq2_bf16": 11,
+    "dq2_res_bf16add": 12,
 }
 
 # Every symbol of include/mk.h with its (restype, argtypes).
@@ -55,6 +56,7 @@ SIGNATURES = {
     "mk_attn_scratch_bytes": (_SZ, [_I, _I, _I, _I]),
     "mk_attn_prefill": (_I, [_P, _P, _P, _P, _P, _SZ, _I, _I, _I, _I, _I, _F, _P]),
     "mk_row_quant": (_I, [_P, _I, _P, _I, _I, _F, _I, _I, _P, _P, _P]),
+    "mk_act_quant": (_I, [_P, _I, _P, _I, _I, _F, _I, _I, _P, _P, _P]),
     "mk_gemm": (_I, [_I, _I, _P, _I, _P, _I, _I, _I, _I, _P, _I, _P, _I, _P, _P, _P, _P]),
     "mk_lm_head": (_I, [_P, _P, _I, _I, _I, _P, _P]),
     "mk_pack_weight": (_I, [_P, _I, _P, _I, _I, _I, _I, _I, _I, _P]),

@@ -81,11 +81,11 @@ class NotEligible(RuntimeError):
 
 
 def mk_seq_ok(seq: int, max_seq: int) -> bool:
-    """The reference's fast-path length rule (model.py:131-136) intersected with libmk's (seq % 256)."""
+    """The reference's fast-path length rule (model.py:131-136): <= 1024 -> multiple of 128, else of
+    1024 (libmk itself serves every multiple of 128)."""
     if seq <= 0 or seq > max_seq:
         return False
-    ok_ref = seq % 128 == 0 if seq <= 1024 else seq % 1024 == 0
-    return ok_ref and seq % 256 == 0
+    return seq % 128 == 0 if seq <= 1024 else seq % 1024 == 0
 
 
 def eligible_batch(prompts, sps, max_seq: int, require_mt1: bool = True):
@@ -100,7 +100,7 @@ def eligible_batch(prompts, sps, max_seq: int, require_mt1: bool = True):
         if not sampling_fast_ok(sp):
             raise NotEligible("unsupported_sampling_feature", "sampling feature outside the fast path")
     if not mk_seq_ok(seq, max_seq):
-        raise NotEligible("seq", f"seq {seq} not served (multiple of 256 and 1024 above 1024, <= {max_seq})")
+        raise NotEligible("seq", f"seq {seq} not served (multiple of 128, of 1024 above 1024, <= {max_seq})")
     return len(prompts), seq
 
 

@@ -83,25 +83,51 @@ def row_quant(x: torch.Tensor, a: torch.Tensor | None, eps: float = 1e-6, norm: 
     return q, sx
 
 
+ACT_MODES = {"int8d": 0, "fp8d": 1, "int8": 2, "fp8": 3}
+FP8 = torch.float8_e4m3fn
+
+
+def act_quant(x: torch.Tensor, a: torch.Tensor | None, mode: str, eps: float = 1e-6, norm: bool = False,
+              recip: bool = False, smul: bool = False):
+    """Activation quantisation in one of the reference's modes (include/mk.h, mk_act_quant): returns
+    (q (T, H) int8 or float8_e4m3fn, sx f32 (T,))."""
+    lib = load()
+    if mode not in ACT_MODES:
+        raise MkError(f"act_quant: unknown mode {mode!r}")
+    if x.dim() != 2 or x.dtype not in (BF16, torch.float32):
+        raise MkError("act_quant: x must be (T, H) bf16 or f32")
+    T, H = x.shape
+    _need(x, "x")
+    if a is not None:
+        _need(a, "a", torch.float32, (H,))
+    q = torch.empty((T, H), dtype=FP8 if mode.startswith("fp8") else torch.int8, device=x.device)
+    sx = torch.empty((T,), dtype=torch.float32, device=x.device)
+    flags = int(norm) | 2 * int(recip) | 4 * int(smul)
+    check(lib.mk_act_quant(_ptr(x), int(x.dtype == torch.float32), _ptr(a), T, H, float(eps), ACT_MODES[mode], flags,
+                           _ptr(q), _ptr(sx), _stream()), "mk_act_quant")
+    return q, sx
+
+
 def gemm(A: torch.Tensor, B: torch.Tensor, epi: str, out: torch.Tensor | None = None, res: torch.Tensor | None = None,
          rs: torch.Tensor | None = None, cs: torch.Tensor | None = None, aux: torch.Tensor | None = None):
     """C = A (M, K) @ B (N, K)^T with a fused epilogue (see include/mk.h MK_EPI_*).
 
-    int8 operands -> int8 MFMA with int32 accumulation; bf16 operands -> bf16 MFMA, f32 accumulation."""
+    int8 operands -> int8 MFMA with int32 accumulation; bf16 / float8_e4m3fn operands -> bf16 / fp8 MFMA,
+    f32 accumulation."""
     lib = load()
     if epi not in EPI:
         raise MkError(f"unknown epilogue {epi!r}")
     if A.dim() != 2 or B.dim() != 2 or A.shape[1] != B.shape[1] or A.dtype != B.dtype:
         raise MkError("gemm: A (M, K) and B (N, K) must share K and dtype")
-    if A.dtype not in (torch.int8, BF16):
-        raise MkError("gemm: operands must be int8 or bf16")
+    if A.dtype not in (torch.int8, BF16, FP8):
+        raise MkError("gemm: operands must be int8, bf16 or float8_e4m3fn")
     _need(A, "A")
     _need(B, "B")
     M, K = A.shape
     N = B.shape[0]
     silu = epi in ("dq_silu", "dq_silu_f32a", "silu_bf16")
     n_out = N // 2 if silu else N
-    residual = epi in ("res_bf16add", "dq_res_bf16add", "res_f32add", "dq2_res_f32add")
+    residual = epi in ("res_bf16add", "dq_res_bf16add", "res_f32add", "dq2_res_f32add", "dq2_res_bf16add")
     if residual:
         if res is None:
             raise MkError("gemm: residual epilogue needs `res`")
@@ -114,7 +140,8 @@ def gemm(A: torch.Tensor, B: torch.Tensor, epi: str, out: torch.Tensor | None = 
     for t, nm, n in ((rs, "rs", M), (cs, "cs", N), (aux, "aux", n_out)):
         if t is not None:
             _need(t, nm, torch.float32, (n,))
-    check(lib.mk_gemm(int(A.dtype == torch.int8), EPI[epi], _ptr(A), K, _ptr(B), K, M, N, K, _ptr(out),
+    in_type = {BF16: 0, torch.int8: 1, FP8: 2}[A.dtype]
+    check(lib.mk_gemm(in_type, EPI[epi], _ptr(A), K, _ptr(B), K, M, N, K, _ptr(out),
                       n_out if out is not None else 0, _ptr(res), N if res is not None else 0, _ptr(rs), _ptr(cs),
                       _ptr(aux), _stream()), "mk_gemm")
     return res if residual else out
@@ -143,4 +170,4 @@ def pack_weight(w: torch.Tensor, map_gu: bool = False, ic: int = 0, inter: int =
     return out
 
 
-__all__ = ["attn_prefill", "attn_scratch_bytes", "row_quant", "gemm", "lm_head", "pack_weight", "MkError", "_lib"]
+__all__ = ["attn_prefill", "attn_scratch_bytes", "row_quant", "act_quant", "gemm", "lm_head", "pack_weight", "MkError", "_lib"]

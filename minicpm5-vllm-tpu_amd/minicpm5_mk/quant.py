@@ -6,8 +6,9 @@ lin in {qkv, o, gu, down}, flags in {sq, lastbf16, fqkv, fmlp}.
 
 `resolve_quant_pair` restates model.py:528-551 for one device (TP = 1): 1B (<= 24 layers)
 "int8d:qkv+gu|sq|lastbf16|fqkv|fmlp", 2B "int8d:qkv+gu+o|sq|lastbf16|fqkv|fmlp"; fmlp only when the
-fused MLP's weights fit (3 * H * I <= 56 MiB).  libmk builds the bf16 and int8d variants; static
-int8 and fp8 activations raise MkError at model creation (MK_EUNSUPPORTED).
+fused MLP's weights fit (3 * H * I <= 56 MiB).  libmk builds every base: bf16, int8d and fp8d
+(per-token dynamic activations), int8 and fp8 (static calibrated activation scales; the down
+projection stays dynamic, mk_jax.py:422-423).
 """
 from __future__ import annotations
 

@@ -34,9 +34,11 @@ def expected_shapes(L: int, H: int, inter: int, n_q: int, n_kv: int, hd: int, qu
     fl = quant_flags(quant)
     Lm, qd = L - 1, n_q * hd
     D = qd + 2 * n_kv * hd
-    i8 = {k: v == "int8d" for k, v in qm.items()}
-    fmlp = "fmlp" in fl and i8["gu"]
-    wt = lambda k: torch.int8 if i8[k] else BF16  # noqa: E731
+    i8 = {k: v != "bf16" for k, v in qm.items()}      # 8-bit weights (int8 or fp8 e4m3)
+    fmlp = "fmlp" in fl and qm["gu"] in ("int8", "int8d")
+    wdt = {"bf16": BF16, "int8": torch.int8, "int8d": torch.int8, "fp8": torch.float8_e4m3fn,
+           "fp8d": torch.float8_e4m3fn}
+    wt = lambda k: wdt[qm[k]]  # noqa: E731
     sc = lambda k, n: (Lm, n) if i8[k] else (Lm, 1)  # noqa: E731
     return {
         "w_qkv": ((Lm, H, D), wt("qkv")), "w_o": ((Lm, qd, H), wt("o")),

@@ -4,11 +4,14 @@ TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).
 
 Each function restates one piece of the reference's device program on the CPU (torch, f32 unless
 stated), with the reference's rounding points:
-  row_quant        mk_mlp.py:161-168 (fused: u * (1/s)), mk_jax.py:257-262 / :283-286 (XLA: u / s)
+  act_quant        activation quantisation of every mode: dynamic int8d / fp8d (mk_mlp.py:161-168,
+                   mk_jax.py:244-250, :257-262, :283-297) and static int8 / fp8 (mk_jax.py:252-256,
+                   :265-268, the bf16-rounded x * rstd of :298-299); row_quant is its int8d case
   int_matmul       exact int8 x int8 -> int64 (the MXU / MFMA int32 accumulation is exact)
+  fp8_matmul       e4m3 x e4m3 products summed exactly (float64), rounded once to f32
   fused_qkv        mk_mlp.py:161-170
-  linear           mk_jax.py:233-269 (bf16 and int8d)
-  linear_rmsnorm   mk_jax.py:272-299 (bf16 and int8d)
+  linear           mk_jax.py:233-269 (bf16, int8d, int8, fp8d, fp8)
+  linear_rmsnorm   mk_jax.py:272-299 (bf16, int8d, fp8d; int8 / fp8 through the bf16 x * rstd)
   fused_mlp        mk_mlp.py:68-97 (bf16 and int8 W_down)
   attention        mk_attn.py:557-657 numerics: RoPE'd q * log2(e) (and the softmax scale) rounded
                    to bf16, RoPE'd k rounded to bf16, scores f32, p = exp2(s - m) rounded to bf16 for
@@ -40,20 +43,58 @@ def bf(x: torch.Tensor) -> torch.Tensor:
 
 
 # ------------------------------------------------------------------------------------------ quant
-def row_quant(x: torch.Tensor, a: torch.Tensor | None, eps: float, norm: bool, recip: bool):
-    """x (T, H) f32 -> (q int8 (T, H), sx f32 (T,)).  sx = s_u * rstd (rstd = 1 without norm)."""
+FP8 = torch.float8_e4m3fn
+
+
+def act_quant(x: torch.Tensor, a: torch.Tensor | None, eps: float, mode: str, norm: bool, recip: bool = False,
+              smul: bool = False):
+    """x (T, H) -> (q (T, H) int8 or float8_e4m3fn, sx f32 (T,)); rstd = rsqrt(mean(x^2) + eps) with norm.
+
+    dynamic (int8d, fp8d): u = x * a; s = max(amax * (1/qmax), 1e-6) (smul) or max(amax / qmax, 1e-6);
+      q = u * (1/s) (recip) or u / s; sx = s * rstd.
+    static (int8, fp8): t = bf16(x * rstd) with norm, else x; q = t * a; sx = 1.
+    int8: clip(round_half_even(q), +-127); fp8: e4m3(clip(q, +-448)) with round-to-nearest-even."""
     x = x.to(F32)
+    fp8 = mode in ("fp8", "fp8d")
+    qmax = 448.0 if fp8 else 127.0
     rstd = torch.rsqrt((x * x).mean(-1, keepdim=True) + eps) if norm else torch.ones_like(x[:, :1])
-    u = x * a if a is not None else x
-    amax = u.abs().amax(-1, keepdim=True)
-    if recip:
-        s = torch.clamp(amax * torch.tensor(1.0 / 127.0, dtype=F32), min=1e-6)
-        q = torch.round(u * (1.0 / s))
+    if mode in ("int8d", "fp8d"):
+        u = x * a if a is not None else x
+        amax = u.abs().amax(-1, keepdim=True)
+        if smul:
+            s = torch.clamp(amax * torch.tensor(1.0 / qmax, dtype=F32), min=1e-6)
+        else:
+            s = torch.clamp(amax / qmax, min=1e-6)
+        t = u * (1.0 / s) if recip else u / s
+        sx = (s * rstd).squeeze(-1)
+    elif mode in ("int8", "fp8"):
+        t = bf(x * rstd) if norm else x
+        t = t * a if a is not None else t
+        sx = torch.ones(x.shape[0], dtype=F32)
     else:
-        s = torch.clamp(amax / 127.0, min=1e-6)
-        q = torch.round(u / s)
-    q = torch.clamp(q, -127, 127).to(torch.int8)
-    return q, (s * rstd).squeeze(-1)
+        raise ValueError(f"act_quant: unknown mode {mode!r}")
+    if fp8:
+        q = torch.clamp(t, -448.0, 448.0).to(FP8)
+    else:
+        q = torch.clamp(torch.round(t), -127, 127).to(torch.int8)
+    return q, sx
+
+
+def row_quant(x: torch.Tensor, a: torch.Tensor | None, eps: float, norm: bool, recip: bool):
+    """Dynamic int8 (act_quant's int8d): the fused prologue (recip: s = amax * (1/127), q = u * (1/s),
+    mk_mlp.py:161-168) or the XLA linear (s = amax / 127, q = u / s, mk_jax.py:257-262)."""
+    return act_quant(x, a, eps, "int8d", norm, recip=recip, smul=recip)
+
+
+def fp8_matmul(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """e4m3 (M, K) @ e4m3 (K, N) -> f32.  Every product has <= 8 significant bits within 2^-18 .. 2^18,
+    so float64 sums them exactly for K < 2^17; the result is rounded once to f32."""
+    return (a.to(torch.float64) @ b.to(torch.float64)).to(F32)
+
+
+def qmatmul(q: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """The 8-bit GEMM of a quantised linear, as f32: exact int32 for int8, fp8_matmul for e4m3."""
+    return fp8_matmul(q, w) if q.dtype == FP8 else int_matmul(q, w).to(F32)
 
 
 def int_matmul(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
@@ -74,26 +115,37 @@ def fused_qkv(x: torch.Tensor, w: torch.Tensor, s_w: torch.Tensor, a: torch.Tens
     return ((acc * sx[:, None]) * s_w.reshape(1, -1)).to(BF16)
 
 
-def linear(x: torch.Tensor, w: torch.Tensor, s_w, a_x, quant: str) -> torch.Tensor:
-    """bf16: bf16(x @ w) in f32;  int8d: per-token dynamic quant of x * a_x, bf16((acc * s_x) * s_w)."""
+def linear(x: torch.Tensor, w: torch.Tensor, s_w, a_x, quant: str, dynamic_act: bool = False) -> torch.Tensor:
+    """mk_jax.py:233-269.  bf16: bf16(x @ w);  int8d: bf16((acc * s_x) * s_w) with s = amax / 127, q = u / s;
+    fp8d: bf16(acc * (s_x * s_w)) with s = amax * (1/448), q = u * (1/s);  static int8 / fp8: bf16(acc * s_w)
+    of q = x * a_x.  dynamic_act turns the static modes dynamic (the down projection, mk_jax.py:422-423)."""
     if quant == "bf16":
         return (x.to(F32) @ w.to(F32)).to(BF16)
-    if quant == "int8d":
-        q, sx = row_quant(x.to(F32), a_x, 0.0, norm=False, recip=False)
-        acc = int_matmul(q, w).to(F32)
-        return ((acc * sx[:, None]) * s_w.reshape(1, -1)).to(BF16)
+    if quant == "int8d" or (quant == "int8" and dynamic_act):
+        q, sx = act_quant(x, a_x, 0.0, "int8d", norm=False)
+        return ((qmatmul(q, w) * sx[:, None]) * s_w.reshape(1, -1)).to(BF16)
+    if quant == "fp8d" or (quant == "fp8" and dynamic_act):
+        q, sx = act_quant(x, a_x, 0.0, "fp8d", norm=False, recip=True, smul=True)
+        return (qmatmul(q, w) * (sx[:, None] * s_w.reshape(1, -1))).to(BF16)
+    if quant in ("int8", "fp8"):
+        q, _ = act_quant(x, a_x, 0.0, quant, norm=False)
+        return (qmatmul(q, w) * s_w.reshape(1, -1)).to(BF16)
     raise NotImplementedError(quant)
 
 
 def linear_rmsnorm(x: torch.Tensor, w: torch.Tensor, s_w, a_x, eps: float, quant: str) -> torch.Tensor:
+    """mk_jax.py:272-299.  Dynamic modes: s = amax * (1/qmax), q = u / s, bf16(acc * (s * rstd * s_w));
+    bf16 / static modes: the linear of bf16(x * rstd)."""
     xf = x.to(F32)
     if quant == "bf16":
         rstd = torch.rsqrt((xf * xf).mean(-1, keepdim=True) + eps)
         return (bf(xf * rstd) @ w.to(F32)).to(BF16)
-    if quant == "int8d":
-        q, sx = row_quant(xf, a_x, eps, norm=True, recip=False)
-        acc = int_matmul(q, w).to(F32)
-        return (acc * (sx[:, None] * s_w.reshape(1, -1))).to(BF16)
+    if quant in ("int8d", "fp8d"):
+        q, sx = act_quant(xf, a_x, eps, quant, norm=True, recip=False, smul=True)
+        return (qmatmul(q, w) * (sx[:, None] * s_w.reshape(1, -1))).to(BF16)
+    if quant in ("int8", "fp8"):
+        q, _ = act_quant(xf, a_x, eps, quant, norm=True)
+        return (qmatmul(q, w) * s_w.reshape(1, -1)).to(BF16)
     raise NotImplementedError(quant)
 
 
@@ -221,14 +273,14 @@ def last_layer_step(x: torch.Tensor, w: dict, cos, sin, n_q: int, n_kv: int, hd:
 def mk_forward(ids: torch.Tensor, w: dict, embed: torch.Tensor, final_norm: torch.Tensor, cfg, quant: str,
                lm_head: torch.Tensor | None = None):
     """ids (B, S) -> (hidden (B, H) bf16, logits (B, V) f32 or None).  `w` is prepare_mk_weights' dict;
-    supports the bf16 / int8d linears with the fused (fqkv, fmlp) or XLA algebra like libmk."""
+    supports every quant base (bf16, int8d, int8, fp8d, fp8) with the fused (fqkv, fmlp) or XLA algebra."""
     from minicpm5_mk.mk_weights import mlp_chunk
     from minicpm5_mk.quant import parse_quant, quant_flags
 
     qm = parse_quant(quant)
     fl = quant_flags(quant)
     fqkv = "fqkv" in fl and qm["qkv"] == "int8d"
-    fmlp = "fmlp" in fl and qm["gu"] == "int8d"
+    fmlp = "fmlp" in fl and qm["gu"] in ("int8", "int8d")
     B, S = ids.shape
     H, n_q, n_kv, hd, eps = cfg.hidden, cfg.n_q, cfg.n_kv, cfg.head_dim, cfg.eps
     inter = cfg.inter
@@ -251,7 +303,8 @@ def mk_forward(ids: torch.Tensor, w: dict, embed: torch.Tensor, final_norm: torc
             sgu = w["s_gu"][l].reshape(-1)
             gu = linear_rmsnorm(x, wgu, sgu, w["a_gu"][l], eps, qm["gu"]).to(F32).view(-1, 2, inter)
             hid = bf(bf(silu_f32(gu[:, 0])) * gu[:, 1]).to(BF16)
-            dn = linear(hid, w["w_down"][l], w["s_down"][l], w["a_down"][l], qm["down"])
+            dn = linear(hid, w["w_down"][l], w["s_down"][l], w["a_down"][l], qm["down"],
+                        dynamic_act=qm["down"] in ("int8", "fp8"))
             x = bf(x.to(F32) + dn.to(F32)).to(BF16)
     x_last = last_layer_step(x.view(B, S, H), w, cos, sin, n_q, n_kv, hd, eps)
     hidden = (_rms_unit_bf16(x_last, eps) * final_norm.to(F32)).to(BF16)

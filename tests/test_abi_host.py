@@ -47,12 +47,14 @@ def _cfg(**kw):
     ({}, b"int8d:qkv+gu|sq|lastbf16|fqkv|fmlp", 1, 8192, 0, ""),
     ({}, b"bf16", 32, 8192, 0, ""),
     ({"head_dim": 96}, b"int8d", 4, 2048, 0, ""),
-    ({}, b"fp8d", 1, 8192, -3, "not built"),
-    ({}, b"int8", 1, 8192, -3, "not built"),
+    ({}, b"fp8d", 1, 8192, 0, ""),
+    ({}, b"int8|fmlp", 1, 8192, 0, ""),
+    ({}, b"fp8:qkv+o|sq", 1, 8192, 0, ""),
     ({}, b"int4", 1, 8192, -1, "unknown base"),
     ({}, b"int8d:qkv+mlp", 1, 8192, -1, "unknown linear"),
     ({}, b"int8d|fast", 1, 8192, -1, "unknown flag"),
-    ({}, b"bf16", 1, 8000, -1, "multiple of 256"),
+    ({}, b"bf16", 1, 8000, -1, "multiple of 128"),
+    ({}, b"bf16", 1, 64, -1, "multiple of 128"),
     ({}, b"bf16", 1, 16384, -1, "max_seq"),
     ({}, b"bf16", 0, 8192, -1, "bs"),
     ({"n_q": 12}, b"bf16", 1, 8192, -1, "8 * n_kv"),
@@ -96,9 +98,9 @@ def test_sampling_fast_ok_and_eligibility():
                 {"repetition_penalty": 1.1}, {"min_p": 0.1}, {"logit_bias": {1: 1.0}}, {"allowed_token_ids": [1]},
                 {"bad_words": ["x"]}, {"structured_outputs": object()}, {"logits_processors": [print]}):
         assert not sampling_fast_ok(SamplingParams(**bad)), bad
-    # the reference rule: <= 1024 -> % 128, else % 1024; libmk adds % 256
-    assert [mk_seq_ok(s, 8256) for s in (128, 256, 768, 1024, 2048, 3072, 8192, 9216, 0)] == \
-        [False, True, True, True, True, True, True, False, False]
+    # the reference rule: <= 1024 -> % 128, else % 1024
+    assert [mk_seq_ok(s, 8256) for s in (128, 384, 896, 1024, 1152, 2048, 3072, 8192, 9216, 0)] == \
+        [True, True, True, True, False, True, True, True, False, False]
     sp = SamplingParams()
     assert eligible_batch([[1] * 1024] * 3, [sp] * 3, 8256) == (3, 1024)
     for prompts, sps, reason in (([[1] * 1024, [1] * 2048], [sp, sp], "ragged"),

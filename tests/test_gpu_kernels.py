@@ -9,6 +9,13 @@
     1 bf16 ulp of the oracle (f32 products identical up to the row scale's last bit).
   * bf16 GEMM: f32 accumulation in a different order than the CPU: relative error <= 1e-2 of the
     output scale, bf16 rounding of the result dominating.
+  * activation quantisation in the fp8d / int8 / fp8 modes: bit-exact codes (the static modes with
+    RMSNorm round x * rstd to bf16, so an rstd one f32 ulp off may move a code by one step: at most
+    0.1% of codes, each by one step); f32 -> e4m3 conversion bit-exact over every finite bf16 value.
+  * fp8 GEMM: v_mfma_f32_32x32x16_fp8_fp8 sums its 16 products at reduced internal precision (measured
+    on MI355X: max error 2.4e-5 of sum|products| at K = 64, 1.5e-6 at K = 4608, zero when the products
+    span few binades), so the bound is 1e-4 * sum|products| of the exact (float64) result; dequant
+    epilogues within 1 bf16 ulp + that bound.
 """
 import math
 
@@ -34,6 +41,7 @@ def _attn_inputs(B, S, hd, n_q=16, n_kv=2):
 
 
 @pytest.mark.parametrize("B,S,hd,theta", [(1, 256, 64, 1e4), (2, 512, 96, 1e4), (1, 1024, 128, 5e6),
+                                           (3, 128, 128, 5e6), (2, 384, 96, 1e4), (1, 640, 128, 5e6),
                                            (1, 8192, 96, 1e4), (1, 8192, 128, 5e6)])
 def test_attention_vs_fp32(B, S, hd, theta):
     from minicpm5_mk import ops
@@ -293,3 +301,119 @@ def test_decoder_block_int8(smooth):
     err = (x2 - x2_r).abs()
     print(f"[block] out max {err.max():.4g} mean {err.mean():.4g}; |out| max {x2_r.abs().max():.3g}", flush=True)
     assert (err <= x2_r.abs() * 2.0 ** -7 + 2e-2).all() and err.mean() <= 1e-3, (float(err.max()), float(err.mean()))
+
+
+# ------------------------------------------------------------------------------------ fp8 / static int8
+@pytest.mark.parametrize("mode,norm,recip,smul", [("fp8d", True, False, True), ("fp8d", False, True, True),
+                                                  ("int8d", True, False, True), ("int8", True, False, False),
+                                                  ("int8", False, False, False), ("fp8", True, False, False),
+                                                  ("fp8", False, False, False)])
+def test_act_quant_modes(mode, norm, recip, smul):
+    from minicpm5_mk import ops
+    from oracle import emulate
+
+    dev = _dev()
+    print(f"[act_quant] {mode} norm={norm} recip={recip} smul={smul}", flush=True)
+    g = torch.Generator().manual_seed(len(mode) * 10 + norm)
+    T, H = 777, 1536
+    x = (torch.randn(T, H, generator=g) * 3).to(BF16)
+    x[0] = 0.0                                      # all-zero row: dynamic scale floor 1e-6
+    x[1, :5] = torch.tensor([1e-30, -5e-3, 300.0, -7.0, 2.0 ** -12]).to(BF16)
+    # static modes: per-channel factors a = 1 / s_x, as prepared weights carry them (large enough to clip)
+    a = (torch.rand(H, generator=g) + 0.5) * (40.0 if mode in ("int8", "fp8") else 1.0)
+    q, sx = ops.act_quant(x.to(dev), a.to(dev), mode, 1e-6, norm, recip, smul)
+    qr, sxr = emulate.act_quant(x.float(), a, 1e-6, mode, norm, recip, smul)
+    q, sx = q.cpu(), sx.cpu()
+    assert q.dtype == qr.dtype
+    if mode.endswith("d"):
+        assert torch.equal(q.view(torch.uint8), qr.view(torch.uint8))
+        if norm:
+            torch.testing.assert_close(sx, sxr, rtol=4e-7, atol=0)
+        else:
+            assert torch.equal(sx, sxr)
+    else:
+        assert torch.equal(sx, torch.ones(T))
+        if mode == "int8":
+            d = (q.to(torch.int32) - qr.to(torch.int32)).abs()
+        else:   # adjacent e4m3 codes of one sign differ by one in their magnitude bits
+            d = (q.view(torch.uint8).to(torch.int32) - qr.view(torch.uint8).to(torch.int32)).abs()
+        if norm:
+            assert d.max() <= 1 and (d > 0).float().mean() <= 1e-3, (int(d.max()), float((d > 0).float().mean()))
+        else:
+            assert d.max() == 0
+
+
+def test_fp8_conversion_exhaustive():
+    """Every finite bf16 value, clipped to +-448, through the hardware e4m3 conversion (static fp8, a = 1)
+    vs torch's round-to-nearest-even float8_e4m3fn cast."""
+    from minicpm5_mk import ops
+
+    dev = _dev()
+    bits = torch.arange(65536, dtype=torch.int32).to(torch.int16)
+    x = bits.view(BF16).reshape(256, 256).clone()
+    x[~torch.isfinite(x.float())] = 0.0
+    q, _ = ops.act_quant(x.to(dev), None, "fp8", 0.0, False)
+    ref = torch.clamp(x.float(), -448.0, 448.0).to(torch.float8_e4m3fn)
+    qb, rb = q.cpu().view(torch.uint8), ref.view(torch.uint8)
+    bad = (qb != rb).nonzero()
+    assert bad.numel() == 0, [(float(x[i, j]), int(qb[i, j]), int(rb[i, j])) for i, j in bad[:8].tolist()]
+
+
+def _fp8_pair(M, N, K, seed):
+    g = torch.Generator().manual_seed(seed)
+    a = (torch.randn(M, K, generator=g) * 40).clamp(-448, 448).to(torch.float8_e4m3fn)
+    b = (torch.randn(N, K, generator=g) * 40).clamp(-448, 448).to(torch.float8_e4m3fn)
+    return a, b
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 128, 64), (300, 200, 1536), (8192, 1920, 1536), (13, 4096, 2048)])
+def test_gemm_fp8(M, N, K):
+    from minicpm5_mk import ops
+    from oracle import emulate
+
+    dev = _dev()
+    a, b = _fp8_pair(M, N, K, M + N)
+    out = ops.gemm(a.to(dev), b.to(dev), "f32").cpu()
+    ref = emulate.fp8_matmul(a, b.t().contiguous())
+    bound = a.to(torch.float64).abs() @ b.to(torch.float64).abs().t()
+    err = (out.double() - ref.double()).abs()
+    assert (err <= 1e-4 * bound).all(), float((err / bound.clamp(min=1e-30)).max())
+
+
+@pytest.mark.parametrize("epi", ["dq2_bf16", "dq2_res_bf16add", "dq_res_bf16add", "silu_bf16"])
+def test_gemm_fp8_epilogues(epi):
+    from minicpm5_mk import ops
+    from oracle import emulate
+
+    dev = _dev()
+    M, N, K = 1000, 512, 1536
+    a, b = _fp8_pair(M, N, K, 17)
+    g = torch.Generator().manual_seed(18)
+    rs = torch.rand(M, generator=g) * 1e-3
+    cs = torch.rand(N, generator=g) * 1e-3
+    acc = emulate.fp8_matmul(a, b.t().contiguous())
+    bound = (a.to(torch.float64).abs() @ b.to(torch.float64).abs().t()).float() * 1e-4
+    x = torch.randn(M, N, generator=g).to(BF16)
+    kw = dict(rs=rs.to(dev), cs=cs.to(dev))
+    if epi == "dq2_bf16":
+        out = ops.gemm(a.to(dev), b.to(dev), epi, **kw).float().cpu()
+        ref = acc * (rs[:, None] * cs[None, :])
+        scale = rs[:, None] * cs[None, :]
+    elif epi == "silu_bf16":
+        out = ops.gemm(a.to(dev), b.to(dev), epi, **kw).float().cpu()   # (M, N/2), 32-column g/u blocks
+        gu = (acc * (rs[:, None] * cs[None, :])).to(BF16).float().view(M, -1, 2, 32)
+        gv, uv = gu[:, :, 0].reshape(M, -1), gu[:, :, 1].reshape(M, -1)
+        ref = (gv / (1 + torch.exp(-gv))).to(BF16).float() * uv
+        tol = ref.abs() * 2.0 ** -6 + 1e-6
+        assert ((out - ref).abs() <= tol).all()
+        return
+    else:
+        out = ops.gemm(a.to(dev), b.to(dev), epi, res=x.clone().to(dev), **kw).float().cpu()
+        o = acc * (rs[:, None] * cs[None, :]) if epi == "dq2_res_bf16add" else (acc * rs[:, None]) * cs[None, :]
+        ref = (x.float() + o.to(BF16).float())
+        scale = rs[:, None] * cs[None, :]
+        tol = (x.float().abs() + o.abs()) * 2.0 ** -7 + bound * scale + 1e-30
+        assert ((out - ref).abs() <= tol).all()
+        return
+    tol = ref.abs() * 2.0 ** -7 + bound * scale + 1e-30
+    assert ((out - ref).abs() <= tol).all()

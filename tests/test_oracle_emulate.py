@@ -2,7 +2,12 @@
 
   * row_quant: brute force per element in pure Python (round-half-even, +-127 clamp, 1e-6 floor,
     all-zero rows, the two reciprocal / division variants of mk_mlp.py:73-76 vs mk_jax.py:259-262);
-  * int_matmul: exact int64 products;
+  * act_quant (fp8d, int8, fp8, and int8d with amax * (1/127)): brute force per element in numpy f32,
+    with e4m3 codes found by nearest-value search over the 254 finite codes of the format's definition
+    (ties to the even code);
+  * int_matmul: exact int64 products;  fp8_matmul: exact rational sums (fractions) on a small case;
+  * linear / linear_rmsnorm in the fp8 and static int8 modes: equal to the float product with the
+    dequantised weights when the quantisation is lossless (exactly representable inputs);
   * fused_qkv: dequantised result within the quantisation error bound of the f32 product
     rmsnorm(x) a (W_q s_w), and exact on an exactly representable case;
   * attention: the emulation and the FP32 reference vs a brute-force per-query softmax loop;
@@ -187,3 +192,134 @@ def test_quantized_model_close_to_fp32_golden(quant):
     gold = torch.from_numpy(fx["logits"])
     assert (lg - gold).abs().max() < 0.05
     assert torch.equal(lg.argmax(-1), gold.argmax(-1))
+
+
+# ---------------------------------------------------------------------------------------- fp8 / static modes
+def _e4m3_table():
+    """(code, value) of every finite float8_e4m3fn code from the format's definition: sign, 4 exponent bits
+    (bias 7), 3 mantissa bits; exponent 0 is subnormal (m / 8 * 2^-6); 0x7f / 0xff are NaN."""
+    out = []
+    for code in range(256):
+        if code & 0x7F == 0x7F:
+            continue
+        sgn = -1.0 if code & 0x80 else 1.0
+        e, m = (code >> 3) & 0xF, code & 7
+        v = (m / 8.0) * 2.0 ** -6 if e == 0 else (1 + m / 8.0) * 2.0 ** (e - 7)
+        out.append((code, sgn * v))
+    return out
+
+
+_E4M3 = _e4m3_table()
+
+
+def _e4m3_rne(v: float) -> int:
+    """Nearest e4m3 code to v (|v| <= 448), ties to the even code; zero keeps the sign of v."""
+    if v == 0.0:
+        return 0x80 if math.copysign(1.0, v) < 0 else 0
+    best = min(abs(v - x) for _, x in _E4M3)
+    cands = [c for c, x in _E4M3 if abs(v - x) == best]
+    if len(cands) > 1:   # a tie between two values (or +-0): the even mantissa, the sign of v for zero
+        cands = [c for c in cands if c & 1 == 0] or cands
+        if len(cands) > 1:
+            cands = [c for c in cands if (c & 0x80 != 0) == (v < 0)]
+    return cands[0]
+
+
+def test_e4m3_table_known_values():
+    assert len(_E4M3) == 254
+    vals = dict(_E4M3)
+    assert vals[0x7E] == 448.0 and vals[0x38] == 1.0 and vals[0x01] == 2.0 ** -9 and vals[0x08] == 2.0 ** -6
+    assert _e4m3_rne(1.0625) == 0x38 and _e4m3_rne(1.1875) == 0x3A      # ties: to the even mantissa
+    assert _e4m3_rne(2.0 ** -10) == 0 and _e4m3_rne(-2.0 ** -10) == 0x80  # half the smallest subnormal -> 0
+    assert _e4m3_rne(232.0) == 0x76 and _e4m3_rne(-448.0) == 0xFE
+
+
+@pytest.mark.parametrize("mode,norm,recip,smul", [("fp8d", True, False, True), ("fp8d", False, True, True),
+                                                  ("int8d", True, False, True), ("int8", True, False, False),
+                                                  ("int8", False, False, False), ("fp8", True, False, False),
+                                                  ("fp8", False, False, False)])
+def test_act_quant_brute_force(mode, norm, recip, smul):
+    from oracle import emulate
+
+    g = torch.Generator().manual_seed(7)
+    T, H = 4, 40
+    x = (torch.randn(T, H, generator=g) * 3).to(BF16).float()
+    x[3] = 0.0
+    x[2, :4] = torch.tensor([448.0, -0.0078125, 1e-3, 2.5])
+    a = torch.rand(H, generator=g) + 0.5
+    if mode in ("int8", "fp8"):
+        a = a * 30
+    q, sx = emulate.act_quant(x, a, 1e-6, mode, norm, recip, smul)
+    fp8 = mode.startswith("fp8")
+    qmax = np.float32(448.0 if fp8 else 127.0)
+    for t in range(T):
+        xs = [np.float32(v) for v in x[t].tolist()]
+        rstd = np.float32(1.0)
+        if norm:
+            ms = np.float32(np.mean(np.array(xs, dtype=np.float32) ** 2, dtype=np.float32))
+            rstd = np.float32(1.0) / np.float32(math.sqrt(np.float32(ms + np.float32(1e-6))))
+        if mode.endswith("d"):
+            u = [xs[j] * np.float32(a[j]) for j in range(H)]
+            amax = np.float32(max(abs(v) for v in u))
+            s = np.float32(amax * np.float32(1.0 / float(qmax))) if smul else np.float32(amax / qmax)
+            s = max(s, np.float32(1e-6))
+            vals = [u[j] * (np.float32(1.0) / s) if recip else u[j] / s for j in range(H)]
+            assert math.isclose(float(sx[t]), float(s * rstd), rel_tol=2e-7)
+        else:
+            xn = [float(torch.tensor(float(v * rstd)).to(BF16)) if norm else float(v) for v in xs]
+            vals = [np.float32(xn[j]) * np.float32(a[j]) for j in range(H)]
+            assert float(sx[t]) == 1.0
+        for j in range(H):
+            v = float(vals[j])
+            if fp8:
+                exp = _e4m3_rne(max(-448.0, min(448.0, v)))
+                assert int(q[t, j].view(torch.uint8)) == exp, (t, j, v)
+            else:
+                assert int(q[t, j]) == max(-127, min(127, _py_round_half_even(v))), (t, j, v)
+
+
+def test_fp8_matmul_exact():
+    from fractions import Fraction
+
+    from oracle import emulate
+
+    g = torch.Generator().manual_seed(9)
+    a = (torch.randn(3, 300, generator=g) * 100).clamp(-448, 448).to(torch.float8_e4m3fn)
+    b = (torch.randn(300, 2, generator=g) * 100).clamp(-448, 448).to(torch.float8_e4m3fn)
+    a[0] = 448.0
+    b[:, 0] = 2.0 ** -9                              # products spanning 2^-18 .. 2^17.6
+    out = emulate.fp8_matmul(a, b)
+    af, bf_ = a.to(torch.float64).tolist(), b.to(torch.float64).tolist()
+    for i in range(3):
+        for j in range(2):
+            exact = sum(Fraction(af[i][k]) * Fraction(bf_[k][j]) for k in range(300))
+            assert float(out[i, j]) == float(np.float32(float(exact)))
+
+
+@pytest.mark.parametrize("quant", ["fp8", "fp8d", "int8"])
+def test_linear_lossless_cases(quant):
+    """Inputs whose quantisation is lossless: the quantised linear equals the f32 product with the
+    dequantised weights (up to the final bf16 rounding and f32 summation order)."""
+    from minicpm5_mk.mk_weights import quantize_w
+    from oracle import emulate
+
+    g = torch.Generator().manual_seed(12)
+    T, K, N = 6, 64, 48
+    w = torch.randn(K, N, generator=g) * 0.05
+    wq, sw = quantize_w(w, quant, 1.0)
+    wdq = wq.to(torch.float64).float() * sw[None, :]
+    # activations on the code grid: static modes see x * a = small integers (codes), dynamic rows have
+    # amax = qmax * 2^j so that s = 2^j exactly and every u / s is a code
+    codes = torch.randint(-8, 9, (T, K), generator=g).float()
+    if quant == "fp8d":
+        codes[:, 0] = 448.0
+        x = (codes * 2.0 ** -4).to(BF16)
+        a = torch.ones(K)
+        out = emulate.linear(x, wq, sw, a, quant).float()
+        ref = x.float() @ wdq
+    else:
+        a = torch.full((K,), 0.5)
+        x = (codes * 2.0).to(BF16)                   # x * a = codes
+        out = emulate.linear(x, wq, sw, a, quant).float()
+        ref = codes @ wdq
+    assert ((out - ref).abs() <= ref.abs() * 2.0 ** -8 + 1e-6 * ref.abs().max()).all()
