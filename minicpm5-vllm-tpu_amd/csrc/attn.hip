@@ -16,6 +16,8 @@
 //     row max / row sum need only in-lane work plus one exchange between the two lane halves.
 //     The accumulator layout of S^T is exactly the B-operand layout P^T needs for O^T = V^T P^T,
 //     so P never leaves registers.
+#include <type_traits>
+
 #include "kernels.h"
 #include "mk_common.h"
 
@@ -83,6 +85,18 @@ struct AttnSmem {
 // it by more than RESCALE_T (log2 units): p = exp2(s - m) <= 2^8 stays exact in f32 and in bf16's
 // relative precision, and O / l is unchanged by the choice of m.
 constexpr float RESCALE_T = 8.f;
+
+// max / sum of v over lanes l and l ^ 32 (the two halves of a query's keys) without an LDS round trip:
+// v_permlane32_swap exchanges the upper half of its first operand with the lower half of its second,
+// so the two results hold {own, other} in some order on every lane
+__device__ inline float xhalf_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ inline float xhalf_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 template <int HD>
 __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
@@ -218,20 +232,19 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
     auto rowmax_rescale = [&](int kt, f32x16 (&sacc)[2]) {
       const int k0 = kt * KT;
       if (k0 + KT - 1 > t0) {
+        const int lim = tok - k0 - 4 * half;
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = k0 + 32 * c + 8 * (r >> 2) + 4 * half + (r & 3);
-            if (key > tok) sacc[c][r] = -INFINITY;
-          }
+          for (int r = 0; r < 16; ++r)
+            if (32 * c + 8 * (r >> 2) + (r & 3) > lim) sacc[c][r] = -INFINITY;
       }
       float mx = sacc[0][0];
 #pragma unroll
       for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sacc[0][r]);
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[1][r]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      mx = xhalf_max(mx);
       if (__any(mx > m + RESCALE_T)) {
         const float mnew = fmaxf(m, mx);
         const float alpha = fast_exp2(m - mnew);
@@ -283,13 +296,15 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
     qk(0, scur);
     rowmax_rescale(0, scur);
 
-    // ---- steady state: iteration t computes QK(t+1), softmax + PV(t) and stages K(t+2), V(t+1).
+    // ---- steady state: step t computes QK(t+1), softmax + PV(t) and stages K(t+2), V(t+1).
     // The two waves of a SIMD run in step (one barrier per tile), so a wave overlaps its own VALU
     // work with its MFMAs: the QK(t+1) MFMAs are issued with the softmax of tile t (exp2, bf16 P,
     // row sum) interleaved, the PV(t) MFMAs with the row max of tile t+1 interleaved.  Each step is
-    // one MFMA plus a slice of the VALU work; LDS operands are read PF steps ahead.
+    // one MFMA plus a slice of the VALU work; LDS operands are read PF steps ahead.  Only the last
+    // key tile crosses the diagonal, so the causal mask lives in the MASK instance of the step alone.
     constexpr int NQK = 2 * KS, NPV = 4 * DT, NCH = 16, PF = 3;
-    for (int t = 0; t + 1 < nkt; ++t) {
+    auto step = [&](auto mask, int t, const f32x16 (&sc)[2], f32x16 (&sn)[2]) {
+      constexpr bool MASK = decltype(mask)::value;
       gload_k(min(t + 2, nkt - 1));   // the clamped reload at the end lands in a free slot
       gload_v(t + 1);
       const char* ksl = kring + ((t + 1) % L::NK) * L::KBYTES;
@@ -300,33 +315,33 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
       u32x4 kr[NQK];
       u32x4 pb[2][2];
       float psum = 0.f;
-      snext[0] = f32x16{};
-      snext[1] = f32x16{};
+      sn[0] = f32x16{};
+      sn[1] = f32x16{};
 #pragma unroll
       for (int j = 0; j < PF; ++j) kr[j] = kread(j);
 #pragma unroll
       for (int j = 0; j < NQK; ++j) {
         if (j + PF < NQK) kr[j + PF] = kread(j + PF);
-        snext[j % 2] = mfma_bf16_32x32x16(kr[j], qreg[j / 2], snext[j % 2]);
+        sn[j % 2] = mfma_bf16_32x32x16(kr[j], qreg[j / 2], sn[j % 2]);
 #pragma unroll
         for (int k = j * NCH / NQK; k < (j + 1) * NCH / NQK; ++k) {
           const int c = k / 8, s2 = (k / 4) % 2, e = k % 4;
-          const float p0 = fast_exp2(scur[c][8 * s2 + 2 * e] - m);
-          const float p1 = fast_exp2(scur[c][8 * s2 + 2 * e + 1] - m);
+          const float p0 = fast_exp2(sc[c][8 * s2 + 2 * e] - m);
+          const float p1 = fast_exp2(sc[c][8 * s2 + 2 * e + 1] - m);
           pb[c][s2][e] = pack_bf2(p0, p1);
           psum = dot2_bf16_sum(pb[c][s2][e], psum);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
-      const int k0 = (t + 1) * KT;
-      if (k0 + KT - 1 > t0) {
+      if constexpr (MASK) {
+        // key k0 + 32 c + 8 (r / 4) + 4 half + r % 4 is masked when it exceeds tok: compare the
+        // compile-time part of the offset with one per-lane limit
+        const int lim = tok - (t + 1) * KT - 4 * half;
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = k0 + 32 * c + 8 * (r >> 2) + 4 * half + (r & 3);
-            if (key > tok) snext[c][r] = -INFINITY;
-          }
+          for (int r = 0; r < 16; ++r)
+            if (32 * c + 8 * (r >> 2) + (r & 3) > lim) sn[c][r] = -INFINITY;
       }
       const char* vsl = vring + (t % L::NV) * L::VBYTES;
       auto vread = [&](int j) {
@@ -344,12 +359,19 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
         o[dt] = mfma_bf16_32x32x16(vr[j], pb[c][s2], o[dt]);
 #pragma unroll
         for (int k = j * NCH / NPV; k < (j + 1) * NCH / NPV; ++k)
-          mx = fmaxf(mx, fmaxf(snext[k / 8][2 * (k % 8)], snext[k / 8][2 * (k % 8) + 1]));
+          mx = fmaxf(mx, fmaxf(sn[k / 8][2 * (k % 8)], sn[k / 8][2 * (k % 8) + 1]));
+        if (j == NPV / 2) {
+          // K(t+2) and V(t+1) into the slots K(t-1) and V(t-1) left (read in steps t-2 and t-1): their
+          // global loads were issued at the start of the step
+          sstore_k((t + 2) % L::NK);
+          sstore_v((t + 1) % L::NV);
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
       l += psum;
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      mx = xhalf_max(mx);
       if (__any(mx > m + RESCALE_T)) {
+        asm volatile("" ::: "memory");   // a branch, not 4 DT + 1 speculated multiplies per tile
         const float mnew = fmaxf(m, mx);
         const float alpha = fast_exp2(m - mnew);
         l *= alpha;
@@ -357,16 +379,25 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
         for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
         m = mnew;
       }
-      sstore_k((t + 2) % L::NK);
-      sstore_v((t + 1) % L::NV);
       __syncthreads();
+    };
+    using Plain = std::integral_constant<bool, false>;
+    using Diag = std::integral_constant<bool, true>;
+    int t = 0;
+    for (; t + 2 < nkt; ++t) {
+      step(Plain{}, t, scur, snext);
+      scur[0] = snext[0];
+      scur[1] = snext[1];
+    }
+    if (t + 1 < nkt) {   // step nkt - 2: QK of the diagonal tile
+      step(Diag{}, t, scur, snext);
       scur[0] = snext[0];
       scur[1] = snext[1];
     }
     softmax_pv((nkt - 1) % L::NV, scur);
     __syncthreads();   // every wave is done with the rings before the output staging reuses them
 
-    l += __shfl_xor(l, 32, 64);
+    l = xhalf_sum(l);
     const float inv = 1.f / l;
     // stage this wave's (32 tokens x hd) output tile in LDS, then write whole rows with 16-byte stores
     constexpr int OROW = HD * 2 + 16;

@@ -24,6 +24,9 @@ LIB = os.path.join(PKG, "libmk.so")
 ARCH = "gfx950"
 
 SOURCES = ["api.cpp", "model.cpp", "attn.hip", "gemm.hip", "norm.hip", "pack.hip"]
+# attention scores are finite or -inf, never NaN: without NaN semantics the row max needs no
+# canonicalising v_max per MFMA result
+EXTRA = {"attn.hip": ["-fno-honor-nans"]}
 CFLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang",
           "-packed-fp32-ops", "-Wno-unused-result", f"-I{INCLUDE}", f"-I{CSRC}"]
 
@@ -37,7 +40,7 @@ def hipcc() -> str:
 
 def _compile(src: str, verbose: bool) -> str:
     obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
-    cmd = [hipcc(), *CFLAGS, "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [hipcc(), *CFLAGS, *EXTRA.get(src, []), "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
