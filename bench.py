@@ -11,7 +11,9 @@ Extra fields:
                 loop one eager forward of the same shape runs with a HIP event pair around every launch
                 on the model's stream (mk_forward_timed); achieved = algorithmic FLOPs per launch
                 (4 hd n_q S(S+1)/2 per sequence and layer) / average launch time, peak = MI355X dense
-                bf16 2.5 PFLOP/s.
+                bf16 2.5 PFLOP/s.  roofline.attainable: the same against the MFMA-only rate this board
+                sustains with random operands, measured live (mk_bench_mfma_peak): under MFMA load the
+                shader clock falls to ~1.5-1.8 GHz (power limit), well below the 2.4 GHz of the peak.
   kernels       the same for every kernel category: QKV / gate-up GEMMs (int8 MFMA, peak 5.0 POP/s when
                 quantised), O / down (bf16 unless quantised), the row kernels and the LM head (HBM GB/s).
   cpu_baseline  the oracle's FP32 CPU forward (oracle/golden.py, a restatement of the reference's
@@ -31,7 +33,7 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path[:0] = [ROOT, os.path.join(ROOT, "minicpm5-vllm-tpu_amd")]
 
-PEAK = {"bf16": 2516.6, "int8": 5033.2, "hbm": 8000.0}   # MI355X dense TFLOP/s, TOP/s; HBM GB/s
+PEAK = {"bf16": 2516.6, "int8": 5033.2, "fp8": 5033.2, "hbm": 8000.0}   # MI355X dense TFLOP/s, TOP/s; HBM GB/s
 METRIC = "prefill tokens/sec at (B,8192) B=1..32, 1B and 2B arch; p50 ms at (1,8192)"
 # HBM bytes per attn_fwd_kernel launch measured by rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (scaled by a
 # 256 MiB copy's counters) for the default workload; profiles/mfma_util_hbm_1b_b1_s8192.txt
@@ -151,17 +153,17 @@ def model_roofline(eng, cfg, ids):
     T = B * S
     H, I, hd, nq, nkv, V = cfg.hidden, cfg.inter, cfg.head_dim, cfg.n_q, cfg.n_kv, cfg.vocab
     qm = parse_quant(eng.quant)
-    i8 = {k: qm[k] == "int8d" for k in ("qkv", "o", "gu", "down")}
+    prec = {k: ("bf16" if v == "bf16" else "fp8" if v.startswith("fp8") else "int8") for k, v in qm.items()}
+    i8 = {k: v != "bf16" for k, v in prec.items()}   # 8-bit linears: TOP/s against the int8 / fp8 peak
     flat = ids.reshape(-1)
     eng.model.forward_timed(flat, B, S, logits=True)          # first eager pass: code objects, caches
     t = eng.model.forward_timed(flat, B, S, logits=True)
     work = {   # kind -> (algorithmic units per launch, unit, peak)
         "attn": (4.0 * hd * nq * S * (S + 1) / 2 * B, "TFLOP/s", PEAK["bf16"]),
-        "gemm_qkv": (2.0 * T * H * (nq + 2 * nkv) * hd, "TOP/s" if i8["qkv"] else "TFLOP/s",
-                     PEAK["int8" if i8["qkv"] else "bf16"]),
-        "gemm_o": (2.0 * T * nq * hd * H, "TOP/s" if i8["o"] else "TFLOP/s", PEAK["int8" if i8["o"] else "bf16"]),
-        "gemm_gu": (2.0 * T * H * 2 * I, "TOP/s" if i8["gu"] else "TFLOP/s", PEAK["int8" if i8["gu"] else "bf16"]),
-        "gemm_down": (2.0 * T * I * H, "TOP/s" if i8["down"] else "TFLOP/s", PEAK["int8" if i8["down"] else "bf16"]),
+        "gemm_qkv": (2.0 * T * H * (nq + 2 * nkv) * hd, "TOP/s" if i8["qkv"] else "TFLOP/s", PEAK[prec["qkv"]]),
+        "gemm_o": (2.0 * T * nq * hd * H, "TOP/s" if i8["o"] else "TFLOP/s", PEAK[prec["o"]]),
+        "gemm_gu": (2.0 * T * H * 2 * I, "TOP/s" if i8["gu"] else "TFLOP/s", PEAK[prec["gu"]]),
+        "gemm_down": (2.0 * T * I * H, "TOP/s" if i8["down"] else "TFLOP/s", PEAK[prec["down"]]),
         # K and V read and written once: 4 S kv_dim bf16 bytes per sequence
         "attn_prep": (4.0 * T * nkv * hd * 2, "GB/s", PEAK["hbm"]),
         # per-token int8 quantisation of an H-wide bf16 row: 2 H read, H written, 4 B scale
@@ -178,6 +180,33 @@ def model_roofline(eng, cfg, ids):
             rate = units / (ms / n) / (1e6 if unit == "GB/s" else 1e9)   # units per ms -> GB/s or T(FL)OP/s
             e.update({"achieved": round(rate, 1), "unit": unit, "peak": peak, "frac": round(rate / peak, 4)})
         out[k] = e
+    return out
+
+
+def attainable_peaks(iters=3000):
+    """MFMA-only throughput with random operands (mk_bench_mfma_peak) at 1 and 2 waves per SIMD: the
+    rate this board sustains under its power limit, in T(FL)OP/s, with the shader clock it ran at."""
+    import ctypes
+
+    import torch
+
+    from minicpm5_mk import _lib
+
+    lib = _lib.load()
+    nbytes = lib.mk_mfma_peak_scratch_bytes(2)
+    scratch = torch.empty(nbytes, dtype=torch.uint8, device="cuda:0")
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    out = {}
+    for name, in_type in (("bf16", 0), ("int8", 1)):
+        best = None
+        for waves in (1, 2):
+            rate, clk = ctypes.c_double(), ctypes.c_double()
+            _lib.check(lib.mk_bench_mfma_peak(in_type, waves, iters, ctypes.c_void_p(scratch.data_ptr()), nbytes, st,
+                                              ctypes.byref(rate), ctypes.byref(clk)), "mk_bench_mfma_peak")
+            r = {"rate": round(rate.value / 1e12, 1), "clock_ghz": round(clk.value, 3), "waves_per_simd": waves}
+            if best is None or r["rate"] > best["rate"]:
+                best = r
+        out[name] = best
     return out
 
 
@@ -273,10 +302,17 @@ def main():
 
     main_run = run(args.batch, args.steps, args.warmup)
     log(f"[bench] B={args.batch}: {main_run}")
-    kern = None
+    kern = attain = None
     if not args.no_kernels:
         kern = model_roofline(eng, cfg, random_token_ids(args.batch, args.seq, seed=1234).to("cuda:0"))
         log(f"[bench] in-model kernels: {json.dumps(kern)}")
+        attain = attainable_peaks()
+        log(f"[bench] MFMA-only random-operand throughput on this board: {attain}")
+        for k, e in kern.items():
+            if "peak" in e and e["unit"] != "GB/s":
+                ap_ = attain["bf16" if e["unit"] == "TFLOP/s" else "int8"]["rate"]
+                e["attainable"] = ap_
+                e["frac_attainable"] = round(e["achieved"] / ap_, 4)
     sweep = []
     for b in [int(x) for x in args.sweep.split(",") if x.strip()]:
         r = run(b, max(3, min(args.steps, int(80 / b))), 1)
@@ -307,7 +343,10 @@ def main():
                            "frac": a["frac"],
                            "traffic": ATTN_TRAFFIC.get((args.arch, args.batch, args.seq, args.quant)),
                            "kernel": "attn_fwd_kernel",
-                           "avg_ms": round(a["avg_us"] / 1e3, 4), "timing": "in-model, HIP events per launch"}
+                           "avg_ms": round(a["avg_us"] / 1e3, 4), "timing": "in-model, HIP events per launch",
+                           "attainable": {"peak": attain["bf16"]["rate"], "frac": a["frac_attainable"],
+                                          "clock_ghz": attain["bf16"]["clock_ghz"],
+                                          "how": "MFMA-only kernel, random operands, measured live (mk_bench_mfma_peak)"}}
         out["kernels"] = kern
     if cpu:
         out["cpu_baseline"] = cpu

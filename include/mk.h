@@ -228,6 +228,15 @@ int mk_bench_gemm(int in_type, int epi, const void* A, int lda, const void* B, i
                   void* out, int ldo, void* res, int ldr, const float* rs, const float* cs, const float* aux,
                   int iters, void* stream, float* avg_ms);
 
+/* No counterpart in the reference (measurement): MFMA-only throughput with random operands that change
+ * every instruction, waves_per_simd (1..4) waves on every SIMD, iters x 8 MFMAs each.  in_type
+ * MK_IN_BF16 (32x32x16) or MK_IN_INT8 (32x32x32); rate in FLOP/s or OP/s; clock_ghz is the shader
+ * clock measured during the run.  The ceiling a kernel can reach under the board's power limit.
+ * scratch: mk_mfma_peak_scratch_bytes(waves_per_simd) bytes of device memory.  Synchronizes. */
+size_t mk_mfma_peak_scratch_bytes(int waves_per_simd);
+int mk_bench_mfma_peak(int in_type, int waves_per_simd, int iters, void* scratch, size_t scratch_bytes, void* stream,
+                       double* rate, double* clock_ghz);
+
 #ifdef __cplusplus
 }
 #endif

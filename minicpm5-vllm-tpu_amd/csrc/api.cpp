@@ -194,6 +194,17 @@ int mk_bench_gemm(int in_type, int epi, const void* A, int lda, const void* B, i
       static_cast<hipStream_t>(stream), avg_ms);
 }
 
+size_t mk_mfma_peak_scratch_bytes(int waves_per_simd) {
+  return waves_per_simd >= 1 && waves_per_simd <= 4 ? mk::mfma_peak_scratch_bytes(waves_per_simd) : 0;
+}
+
+int mk_bench_mfma_peak(int in_type, int waves_per_simd, int iters, void* scratch, size_t scratch_bytes, void* stream,
+                       double* rate, double* clock_ghz) {
+  MK_REQUIRE(in_type == MK_IN_BF16 || in_type == MK_IN_INT8, "mfma_peak: in_type must be MK_IN_BF16 or MK_IN_INT8");
+  MK_TRY(mk::run_mfma_peak(in_type == MK_IN_INT8, waves_per_simd, iters, scratch, scratch_bytes,
+                           static_cast<hipStream_t>(stream), rate, clock_ghz));
+}
+
 int mk_row_quant(const void* x, int x_f32, const float* a, int T, int H, float eps, int norm, int recip,
                  int8_t* q, float* sx, void* stream) {
   mk::QuantArgs qa{x, H, x_f32 != 0, a, T, H, eps, norm != 0, recip != 0, q, H, sx};

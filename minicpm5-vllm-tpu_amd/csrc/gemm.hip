@@ -19,6 +19,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
+#include <type_traits>
 
 #include "kernels.h"
 #include "mk_common.h"
@@ -306,15 +307,18 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
     __builtin_amdgcn_s_waitcnt(0xc07f);
     if (wm == 1) lds_barrier();
     int cur = 0;
-    auto step = [&](int it, u32x4 (&ha)[NOP], u32x4 (&hb)[NOP], u32x4 (&hc)[NOP]) {
+    // `steady` instances (stage it + D exists) have no runtime conditions, so the compute phase stays one
+    // basic block instead of a branch around every operand read
+    auto step = [&](auto steady, int it, u32x4 (&ha)[NOP], u32x4 (&hb)[NOP], u32x4 (&hc)[NOP]) {
+      constexpr bool ST = decltype(steady)::value;
       // M(it): async loads of stage it + D into the slot of stage it - 1
-      const bool pre = it + D < nk;
+      const bool pre = ST || it + D < nk;
       if (pre) {
         const int nslot = cur == 0 ? C::NST - 1 : cur - 1;
 #pragma unroll
         for (int j = 0; j < Q; ++j) issue1(j, nslot, (it + D) * BKB);
       }
-      if (wm == 0 && it + 1 < nk) {
+      if (wm == 0 && (ST || it + 1 < nk)) {
         if (pre) MK_WAIT_VMCNT((D - 1) * Q);
         else MK_WAIT_VMCNT(0);
       }
@@ -322,7 +326,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
       // C(it): MFMAs of stage it, reads of stage it + 1
       const int s1 = cur == C::NST - 1 ? 0 : cur + 1;
       const char* S1 = smem + s1 * C::ST_BYTES;
-      const bool nxt = it + 1 < nk;
+      const bool nxt = ST || it + 1 < nk;
       __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int i = 0; i < NMF; ++i) {
@@ -344,17 +348,25 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
         if (nxt) rdq(S1, 1, q, ha);
       __builtin_amdgcn_s_setprio(0);
       __builtin_amdgcn_s_waitcnt(0xc07f);                 // lgkmcnt(0): stage it + 1 is in registers
-      if (wm == 1 && it + 2 < nk) {
+      if (wm == 1 && (ST || it + 2 < nk)) {
         if (pre) MK_WAIT_VMCNT((D - 2) * Q);
         else MK_WAIT_VMCNT(0);
       }
       lds_barrier();
       cur = s1;
     };
-    for (int it = 0; it < nk; it += 3) {
-      step(it, H0, H1, H2);
-      if (it + 1 < nk) step(it + 1, H2, H0, H1);
-      if (it + 2 < nk) step(it + 2, H1, H2, H0);
+    using Steady = std::integral_constant<bool, true>;
+    using Tail = std::integral_constant<bool, false>;
+    int it = 0;
+    for (; it + 2 + D < nk; it += 3) {
+      step(Steady{}, it, H0, H1, H2);
+      step(Steady{}, it + 1, H2, H0, H1);
+      step(Steady{}, it + 2, H1, H2, H0);
+    }
+    for (; it < nk; it += 3) {
+      step(Tail{}, it, H0, H1, H2);
+      if (it + 1 < nk) step(Tail{}, it + 1, H2, H0, H1);
+      if (it + 2 < nk) step(Tail{}, it + 2, H1, H2, H0);
     }
     if (wm == 0) lds_barrier();
   } else {
@@ -362,14 +374,15 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
     rd(smem, ao0, bo0, ra0, rb0);
     int cur = 0;                                            // stage slot of iteration it
     constexpr int SPLIT = NMF / 4;                          // k-step 1 MFMAs issued before the barrier
-    for (int it = 0; it < nk; ++it) {
+    auto iter = [&](auto steady, int it) {
+      constexpr bool ST = decltype(steady)::value;
       const char* S = smem + cur * C::ST_BYTES;
       // R0's reads (issued a dozen MFMAs ago) are done; waiting for them here keeps the outstanding LDS
       // reads within what lgkmcnt can count, so the k-step 1 reads below overlap the k-step 0 MFMAs
       __builtin_amdgcn_s_waitcnt(0xc07f);
       rd(S, ao1, bo1, ra1, rb1);
       __builtin_amdgcn_sched_barrier(0);
-      const bool pre = it + C::NST - 1 < nk;
+      const bool pre = ST || it + C::NST - 1 < nk;
       const int nslot = cur == 0 ? C::NST - 1 : cur - 1;    // slot of stage it + NST - 1 (= it - 1)
       const int nkb = (it + C::NST - 1) * BKB;
 #pragma unroll
@@ -386,7 +399,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
       for (int i = 0; i < SPLIT; ++i) mf(i, ra1, rb1);
       __builtin_amdgcn_sched_barrier(0);
       cur = cur == C::NST - 1 ? 0 : cur + 1;
-      if (it + 1 < nk) {
+      if (ST || it + 1 < nk) {
         // stage it + 1 landed for this wave, then for every wave; every wave finished reading stage it
         if (pre) MK_WAIT_VMCNT((C::NST - 2) * Q);
         else MK_WAIT_VMCNT(0);
@@ -397,7 +410,10 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int i = SPLIT; i < NMF; ++i) mf(i, ra1, rb1);
       __builtin_amdgcn_sched_barrier(0);
-    }
+    };
+    int it = 0;
+    for (; it + C::NST - 1 < nk; ++it) iter(std::integral_constant<bool, true>{}, it);
+    for (; it < nk; ++it) iter(std::integral_constant<bool, false>{}, it);
   }
 
   // ---- epilogue through LDS.  The accumulators of a 32x32 tile sit column-wise across lanes (lane:

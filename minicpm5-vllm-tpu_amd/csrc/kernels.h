@@ -127,4 +127,11 @@ struct PackArgs {
 int launch_pack(const PackArgs& p, hipStream_t st);
 int launch_pack_scales(const float* in, float* out, int inter, int ic, hipStream_t st);
 
+// ------------------------------------------------------------------------------ measurement
+// MFMA-only throughput (random operands, 32x32 bf16 or int8) on every SIMD: the rate this board
+// sustains under its power limit, and the shader clock it ran at.
+size_t mfma_peak_scratch_bytes(int waves_per_simd);
+int run_mfma_peak(bool i8, int waves_per_simd, int iters, void* scratch, size_t scratch_bytes, hipStream_t st,
+                  double* rate, double* clock_ghz);
+
 }  // namespace mk

@@ -57,6 +57,8 @@ SIGNATURES = {
     "mk_attn_prefill": (_I, [_P, _P, _P, _P, _P, _SZ, _I, _I, _I, _I, _I, _F, _P]),
     "mk_row_quant": (_I, [_P, _I, _P, _I, _I, _F, _I, _I, _P, _P, _P]),
     "mk_act_quant": (_I, [_P, _I, _P, _I, _I, _F, _I, _I, _P, _P, _P]),
+    "mk_mfma_peak_scratch_bytes": (_SZ, [_I]),
+    "mk_bench_mfma_peak": (_I, [_I, _I, _I, _P, _SZ, _P, _P, _P]),
     "mk_gemm": (_I, [_I, _I, _P, _I, _P, _I, _I, _I, _I, _P, _I, _P, _I, _P, _P, _P, _P]),
     "mk_lm_head": (_I, [_P, _P, _I, _I, _I, _P, _P]),
     "mk_pack_weight": (_I, [_P, _I, _P, _I, _I, _I, _I, _I, _I, _P]),
