@@ -444,87 +444,97 @@ int launch_attn_hd(const AttnArgs& a, hipStream_t st, int stages) {
 }
 
 // ---- last-token attention (mk_jax.py:492-520): one query per sequence against all S keys.
-// Kernel 1: workgroup = (256-key chunk, kv head, sequence); thread = key; the last chunk may be
-// partial (S a multiple of 64).  Writes per (head, chunk) the partial max m, sum l = sum exp(s - m)
-// and o = sum exp(s - m) v.  Kernel 2 merges the chunks.  RoPE (position S-1 for q, the key's position for k) is computed in f32 and rounded to
-// bf16, as apply_rope_4d returns bf16 (mk_jax.py:48-52); scores and softmax are f32.
-constexpr int LCH = 256;
+// Kernel 1: workgroup = (64-key chunk, kv head, sequence), 4 waves; lane = key, wave = pair of q heads.
+// K rows are RoPE'd once into LDS (f32 of the bf16-rounded value, as apply_rope_4d returns bf16,
+// mk_jax.py:48-52); q is RoPE'd at position S-1 and rounded to bf16 likewise.  Scores and softmax are
+// f32 (p not rounded).  Writes per (head, chunk) the partial max m, sum l = sum exp(s - m) and
+// o = sum exp(s - m) v; kernel 2 merges the chunks.
+constexpr int LCH = 64;
 
 template <int HD>
-__global__ __launch_bounds__(LCH) void last_attn_part_kernel(LastAttnArgs a) {
+__global__ __launch_bounds__(256) void last_attn_part_kernel(LastAttnArgs a) {
+  constexpr int H2 = HD / 2, KR = HD + 1;   // padded f32 K row: lanes (keys) hit distinct banks
   __shared__ float qs[G][HD];
+  __shared__ float ks[LCH][KR];
   __shared__ float ps[G][LCH];
-  __shared__ float red[G][LCH / 64];
+  __shared__ __attribute__((aligned(16))) uint16_t vs[LCH][HD];
   const int chunk = blockIdx.x, kv = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
-  const int nchunk = (a.S + LCH - 1) / LCH;
-  const int nkey = min(LCH, a.S - chunk * LCH);   // keys of this chunk (>= 64)
-  constexpr int H2 = HD / 2;
+  const int lane = tid & 63, w = tid >> 6;
+  const int nchunk = a.S / LCH;
+  const int kvdim = a.n_kv * HD;
   const size_t pos_last = (size_t)(a.S - 1) * HD;
-  for (int i = tid; i < G * HD; i += LCH) {
+  for (int i = tid; i < G * HD; i += 256) {
     const int h = i / HD, d = i % HD;
     const uint16_t* q = a.q + ((size_t)b * a.n_q + kv * G + h) * HD;
     const float x = bf2f(q[d]);
     const float y = d < H2 ? -bf2f(q[d + H2]) : bf2f(q[d - H2]);
     qs[h][d] = bf2f(f2bf(x * bf2f(a.cos[pos_last + d]) + y * bf2f(a.sin[pos_last + d])));
   }
-  __syncthreads();
-  const bool valid = tid < nkey;
-  const int t = chunk * LCH + (valid ? tid : 0);
-  const int kvdim = a.n_kv * HD;
-  const uint16_t* krow = a.kv + ((size_t)b * a.S + t) * (2 * kvdim) + kv * HD;
-  float s[G];
+  // K: 16-byte chunks c (8 dims) and their rotate-half partners c + HD / 16, RoPE'd at the key's position
+  const size_t row0 = (size_t)b * a.S + (size_t)chunk * LCH;
+  for (int i = tid; i < LCH * (HD / 16); i += 256) {
+    const int key = i / (HD / 16), c = i % (HD / 16);
+    const uint16_t* krow = a.kv + (row0 + key) * (2 * kvdim) + kv * HD;
+    const u32x4 lo = *reinterpret_cast<const u32x4*>(krow + 8 * c);
+    const u32x4 hi = *reinterpret_cast<const u32x4*>(krow + H2 + 8 * c);
+    const size_t tb = (size_t)(chunk * LCH + key) * HD;
+    const u32x4 cl = *reinterpret_cast<const u32x4*>(a.cos + tb + 8 * c);
+    const u32x4 ch = *reinterpret_cast<const u32x4*>(a.cos + tb + H2 + 8 * c);
+    const u32x4 sl = *reinterpret_cast<const u32x4*>(a.sin + tb + 8 * c);
+    const u32x4 sh = *reinterpret_cast<const u32x4*>(a.sin + tb + H2 + 8 * c);
 #pragma unroll
-  for (int h = 0; h < G; ++h) s[h] = 0.f;
-  for (int d = 0; d < H2 && valid; ++d) {
-    const float x1 = bf2f(krow[d]), x2 = bf2f(krow[d + H2]);
-    const size_t tb = (size_t)t * HD;
-    const float k1 = bf2f(f2bf(x1 * bf2f(a.cos[tb + d]) - x2 * bf2f(a.sin[tb + d])));
-    const float k2 = bf2f(f2bf(x2 * bf2f(a.cos[tb + d + H2]) + x1 * bf2f(a.sin[tb + d + H2])));
-#pragma unroll
-    for (int h = 0; h < G; ++h) s[h] += qs[h][d] * k1 + qs[h][d + H2] * k2;
+    for (int e = 0; e < 8; ++e) {
+      const float x1 = e & 1 ? bf_hi(lo[e / 2]) : bf_lo(lo[e / 2]);
+      const float x2 = e & 1 ? bf_hi(hi[e / 2]) : bf_lo(hi[e / 2]);
+      const float c1 = e & 1 ? bf_hi(cl[e / 2]) : bf_lo(cl[e / 2]);
+      const float c2 = e & 1 ? bf_hi(ch[e / 2]) : bf_lo(ch[e / 2]);
+      const float s1 = e & 1 ? bf_hi(sl[e / 2]) : bf_lo(sl[e / 2]);
+      const float s2 = e & 1 ? bf_hi(sh[e / 2]) : bf_lo(sh[e / 2]);
+      ks[key][8 * c + e] = bf2f(f2bf(x1 * c1 - x2 * s1));
+      ks[key][H2 + 8 * c + e] = bf2f(f2bf(x2 * c2 + x1 * s2));
+    }
   }
-  if (!valid) {
-#pragma unroll
-    for (int h = 0; h < G; ++h) s[h] = -INFINITY;
-  }
-  // block max per head (finite: every chunk holds at least one key)
-  const int lane = tid & 63, w = tid >> 6;
-#pragma unroll
-  for (int h = 0; h < G; ++h) {
-    float v = s[h];
-    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    if (lane == 0) red[h][w] = v;
-  }
-  __syncthreads();
-  float mh[G];
-#pragma unroll
-  for (int h = 0; h < G; ++h) {
-    float v = red[h][0];
-    for (int i = 1; i < LCH / 64; ++i) v = fmaxf(v, red[h][i]);
-    mh[h] = v;
+  for (int i = tid; i < LCH * (HD / 8); i += 256) {
+    const int key = i / (HD / 8), c = i % (HD / 8);
+    *reinterpret_cast<u32x4*>(&vs[key][8 * c]) =
+        *reinterpret_cast<const u32x4*>(a.kv + (row0 + key) * (2 * kvdim) + kvdim + kv * HD + 8 * c);
   }
   __syncthreads();
+  // scores of key `lane` for heads 2w, 2w + 1; max and sum over the chunk's keys within the wave
+  float s0 = 0.f, s1 = 0.f;
+#pragma unroll 8
+  for (int d = 0; d < HD; ++d) {
+    const float kd = ks[lane][d];
+    s0 += qs[2 * w][d] * kd;
+    s1 += qs[2 * w + 1][d] * kd;
+  }
+  float m0 = s0, m1 = s1;
 #pragma unroll
-  for (int h = 0; h < G; ++h) {
-    const float p = __expf(s[h] - mh[h]);
-    ps[h][tid] = p;
-    float v = p;
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-    if (lane == 0) red[h][w] = v;
+  for (int o = 32; o >= 1; o >>= 1) {
+    m0 = fmaxf(m0, __shfl_xor(m0, o, 64));
+    m1 = fmaxf(m1, __shfl_xor(m1, o, 64));
+  }
+  const float p0 = __expf(s0 - m0), p1 = __expf(s1 - m1);
+  ps[2 * w][lane] = p0;
+  ps[2 * w + 1][lane] = p1;
+  float l0 = p0, l1 = p1;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    l0 += __shfl_xor(l0, o, 64);
+    l1 += __shfl_xor(l1, o, 64);
   }
   __syncthreads();
-  const uint16_t* vbase = a.kv + ((size_t)b * a.S + chunk * LCH) * (2 * kvdim) + kvdim + kv * HD;
-  for (int i = tid; i < G * HD; i += LCH) {
-    const int h = i / HD, d = i % HD;
+  // o[h][d] = sum over keys of p[h][key] v[key][d]: thread = (head pair of its wave, d)
+  for (int i = lane; i < 2 * HD; i += 64) {
+    const int h = 2 * w + i / HD, d = i % HD;
     float o = 0.f;
-    for (int k = 0; k < nkey; ++k) o += ps[h][k] * bf2f(vbase[(size_t)k * 2 * kvdim + d]);
+#pragma unroll 8
+    for (int k = 0; k < LCH; ++k) o += ps[h][k] * bf2f(vs[k][d]);
     float* pp = a.part + (((size_t)b * a.n_q + kv * G + h) * nchunk + chunk) * (HD + 2);
     pp[2 + d] = o;
     if (d == 0) {
-      float l = 0.f;
-      for (int j = 0; j < LCH / 64; ++j) l += red[h][j];
-      pp[0] = mh[h];
-      pp[1] = l;
+      pp[0] = h == 2 * w ? m0 : m1;
+      pp[1] = h == 2 * w ? l0 : l1;
     }
   }
 }
@@ -532,7 +542,7 @@ __global__ __launch_bounds__(LCH) void last_attn_part_kernel(LastAttnArgs a) {
 template <int HD>
 __global__ void last_attn_merge_kernel(LastAttnArgs a) {
   const int head = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
-  const int nchunk = (a.S + LCH - 1) / LCH;
+  const int nchunk = a.S / LCH;
   const float* pp = a.part + ((size_t)b * a.n_q + head) * nchunk * (HD + 2);
   float M = -INFINITY;
   for (int c = 0; c < nchunk; ++c) M = fmaxf(M, pp[(size_t)c * (HD + 2)]);
@@ -547,7 +557,7 @@ __global__ void last_attn_merge_kernel(LastAttnArgs a) {
 
 template <int HD>
 int launch_last_attn_hd(const LastAttnArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL(last_attn_part_kernel<HD>, dim3((a.S + LCH - 1) / LCH, a.n_kv, a.B), dim3(LCH), 0, st, a);
+  hipLaunchKernelGGL(last_attn_part_kernel<HD>, dim3(a.S / LCH, a.n_kv, a.B), dim3(256), 0, st, a);
   MK_HIP_CHECK(hipGetLastError());
   hipLaunchKernelGGL(last_attn_merge_kernel<HD>, dim3(a.n_q, a.B), dim3(HD), 0, st, a);
   MK_HIP_CHECK(hipGetLastError());
@@ -588,6 +598,7 @@ size_t last_attn_scratch_bytes(int B, int S, int n_q, int hd) {
 int launch_last_attn(const LastAttnArgs& a, hipStream_t st) {
   int rc = attn_validate(a.B, a.S, a.n_q, a.n_kv, a.hd);
   if (rc) return rc;
+  MK_REQUIRE(a.S % LCH == 0, "last-token attention: seq must be a multiple of 64");
   switch (a.hd) {
     case 64: return launch_last_attn_hd<64>(a, st);
     case 96: return launch_last_attn_hd<96>(a, st);

@@ -550,10 +550,16 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
   }
 }
 
-// ---- skinny GEMM: M <= 32.  One wave per 32 output columns; weights streamed straight from HBM.
+// ---- skinny GEMM: M <= 32 (last-token layer, LM head): weight streaming.  One wave per (32 output
+// columns, K range); every lane keeps SK_U k-steps of weight loads in flight (8 KB per wave) so the
+// weight stream runs near HBM rate.  With a workspace the K range is split over SK > 1 waves per
+// column block: each writes its f32 partial sums, and a second kernel adds them in split order (no
+// atomics: the result does not depend on timing) and applies the epilogue.
 constexpr int SK_WAVES = 4;
-template <GemmIn IN, Epi EPI>
-__global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_kernel(GemmArgs g) {
+constexpr int SK_U = 4;   // k-steps of 64 bytes per lane in flight
+
+template <GemmIn IN, Epi EPI, bool PART>
+__global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_kernel(GemmArgs g, int kchunk, float* part) {
   using T = Mma<IN>;
   using Acc = typename T::Acc;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -561,22 +567,28 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_kernel(GemmArgs g) 
   const int n0 = (blockIdx.x * SK_WAVES + w) * 32;
   if (n0 >= g.N) return;
   const int lda = g.lda * T::ESZ, ldb = g.ldb * T::ESZ, Kb = g.K * T::ESZ;
+  const int kb0 = blockIdx.y * kchunk, kb1 = min(Kb, kb0 + kchunk);
   const bool arow = col < g.M;
   const bool brow = n0 + col < g.N;
   const char* ap = static_cast<const char*>(g.A) + (size_t)(arow ? col : 0) * lda + half * 16;
   const char* bp = static_cast<const char*>(g.B) + (size_t)(brow ? n0 + col : 0) * ldb + half * 16;
+  const u32x4 zero = {0, 0, 0, 0};
   Acc acc0 = Acc{}, acc1 = Acc{};
-  int kb = 0;
-  for (; kb + 64 <= Kb; kb += 64) {
-    const u32x4 a0 = arow ? *reinterpret_cast<const u32x4*>(ap + kb) : u32x4{0, 0, 0, 0};
-    const u32x4 b0 = *reinterpret_cast<const u32x4*>(bp + kb);
-    const u32x4 a1 = arow ? *reinterpret_cast<const u32x4*>(ap + kb + 32) : u32x4{0, 0, 0, 0};
-    const u32x4 b1 = *reinterpret_cast<const u32x4*>(bp + kb + 32);
-    acc0 = T::run(a0, b0, acc0);
-    acc1 = T::run(a1, b1, acc1);
+  int kb = kb0;
+  for (; kb + 64 * SK_U <= kb1; kb += 64 * SK_U) {
+    u32x4 a[2 * SK_U], b[2 * SK_U];
+#pragma unroll
+    for (int u = 0; u < 2 * SK_U; ++u) b[u] = *reinterpret_cast<const u32x4*>(bp + kb + 32 * u);
+#pragma unroll
+    for (int u = 0; u < 2 * SK_U; ++u) a[u] = arow ? *reinterpret_cast<const u32x4*>(ap + kb + 32 * u) : zero;
+#pragma unroll
+    for (int u = 0; u < SK_U; ++u) {
+      acc0 = T::run(a[2 * u], b[2 * u], acc0);
+      acc1 = T::run(a[2 * u + 1], b[2 * u + 1], acc1);
+    }
   }
-  for (; kb < Kb; kb += 32) {
-    const u32x4 a0 = arow ? *reinterpret_cast<const u32x4*>(ap + kb) : u32x4{0, 0, 0, 0};
+  for (; kb < kb1; kb += 32) {
+    const u32x4 a0 = arow ? *reinterpret_cast<const u32x4*>(ap + kb) : zero;
     const u32x4 b0 = *reinterpret_cast<const u32x4*>(bp + kb);
     acc0 = T::run(a0, b0, acc0);
   }
@@ -586,13 +598,25 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_kernel(GemmArgs g) 
   for (int r = 0; r < 16; ++r) {
     const int m = 8 * (r >> 2) + 4 * half + (r & 3);
     if (m >= g.M) continue;
-    const float v = T::f(acc0[r]) + T::f(acc1[r]);
-    if constexpr (EPI == Epi::I32) {
+    if constexpr (PART) {
+      part[((size_t)blockIdx.y * g.M + m) * g.N + n] = T::f(acc0[r]) + T::f(acc1[r]);
+    } else if constexpr (EPI == Epi::I32) {
       static_cast<int32_t*>(g.out)[(size_t)m * g.ldo + n] = static_cast<int32_t>(acc0[r] + acc1[r]);
     } else {
-      epi_store<EPI>(g, m, n, v);
+      epi_store<EPI>(g, m, n, T::f(acc0[r]) + T::f(acc1[r]));
     }
   }
+}
+
+// Sum of the split-K partials in split order, then the epilogue.
+template <Epi EPI>
+__global__ __launch_bounds__(256) void skinny_reduce_kernel(GemmArgs g, int splits, const float* part) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (size_t)g.M * g.N) return;
+  const int m = (int)(i / g.N), n = (int)(i % g.N);
+  float v = 0.f;
+  for (int s = 0; s < splits; ++s) v += part[((size_t)s * g.M + m) * g.N + n];
+  epi_store<EPI>(g, m, n, v);
 }
 
 // Tile configuration for a problem.  The busiest CU runs ceil(tiles / 256) tiles (the order spreads
@@ -651,10 +675,34 @@ void launch_t(const GemmArgs& g, hipStream_t st) {
   }
 }
 
+// K splits of a skinny GEMM: enough waves to keep HBM busy (~2048 over the chip), each split at least
+// 512 bytes of K, at most 16 splits, and the partials within the caller's workspace.  The split depends only on (N, K, M bound),
+// so a row's result is the same for every batch size.
+int skinny_splits(const GemmArgs& g, int esz) {
+  if (!g.ws || g.epi == Epi::I32) return 1;
+  const int nb = (g.N + 31) / 32, Kb = g.K * esz;
+  int sp = std::max(1, std::min(std::min(2048 / std::max(nb, 1), Kb / 512), 16));
+  while (sp > 1 && (size_t)sp * 32 * g.N * sizeof(float) > g.ws_bytes) --sp;
+  return sp;
+}
+
 template <GemmIn IN, Epi EPI>
 void launch_skinny_t(const GemmArgs& g, hipStream_t st) {
-  dim3 grid((g.N + 32 * SK_WAVES - 1) / (32 * SK_WAVES));
-  hipLaunchKernelGGL((gemm_skinny_kernel<IN, EPI>), grid, dim3(64 * SK_WAVES), 0, st, g);
+  const int esz = IN == GemmIn::BF16 ? 2 : 1;
+  const int sp = skinny_splits(g, esz);
+  const int Kb = g.K * esz;
+  const int kchunk = ((Kb + sp - 1) / sp + 63) / 64 * 64;
+  const int splits = (Kb + kchunk - 1) / kchunk;
+  dim3 grid((g.N + 32 * SK_WAVES - 1) / (32 * SK_WAVES), splits);
+  if (splits == 1) {
+    hipLaunchKernelGGL((gemm_skinny_kernel<IN, EPI, false>), grid, dim3(64 * SK_WAVES), 0, st, g, kchunk, nullptr);
+  } else {
+    float* part = static_cast<float*>(g.ws);
+    hipLaunchKernelGGL((gemm_skinny_kernel<IN, EPI, true>), grid, dim3(64 * SK_WAVES), 0, st, g, kchunk, part);
+    const size_t n = (size_t)g.M * g.N;
+    hipLaunchKernelGGL((skinny_reduce_kernel<EPI>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, g, splits,
+                       part);
+  }
 }
 
 // Epilogues built per operand type: fp8 operands only come with the dequantising epilogues of the

@@ -69,11 +69,14 @@ struct GemmArgs {
   int cfg;                    // tile configuration: 0 auto, 1 256x256 (4 waves), 2 256x128, 3 128x128,
                               // 4 256x256 (8 waves)
   int gm;                     // tile-order group height (rows of tiles); 0 = chosen by the launcher
+  void* ws;                   // skinny GEMM: optional f32 workspace for split-K partials (null = no split)
+  size_t ws_bytes;
 };
 int gemm_validate(const GemmArgs& g);
 int launch_gemm(const GemmArgs& g, hipStream_t st);
 
-// Skinny GEMM for M <= 32 rows (last-token layer, LM head): same math, weights streamed once.
+// Skinny GEMM for M <= 32 rows (last-token layer, LM head): same math, weights streamed once; with
+// g.ws, the K range is split over more waves (partials summed in a fixed order by a second kernel).
 int launch_gemm_skinny(const GemmArgs& g, hipStream_t st);
 
 // ------------------------------------------------------------------------------ norm / quant

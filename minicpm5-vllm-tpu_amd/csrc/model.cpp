@@ -186,6 +186,9 @@ int workspace_layout(const Model& m, int B, int S, WorkLayout* W) {
   W->xl = take((size_t)B * H * 2);
   W->gul = take((size_t)B * 2 * I * 2);
   W->hl = take((size_t)B * I * 2);
+  // split-K partials of the last layer's skinny GEMMs: up to 16 splits x 32 rows x the widest output
+  W->skws_bytes = (size_t)16 * 32 * std::max(std::max(qd, H), 2 * I) * sizeof(float);
+  W->skws = take(W->skws_bytes);
   W->total = off;
   return MK_OK;
 }
@@ -545,6 +548,8 @@ int launch_forward(const Fwd& f, hipStream_t st) {
     g.K = H;
     g.out = ql + (size_t)b0 * qd;
     g.ldo = qd;
+    g.ws = ws + f.W.skws;
+    g.ws_bytes = f.W.skws_bytes;
     MK_RUN(launch_gemm_skinny(g, st));
   }
   {
@@ -576,6 +581,8 @@ int launch_forward(const Fwd& f, hipStream_t st) {
     g.epi = Epi::RES_BF16ADD;
     g.res = xl + (size_t)b0 * H;
     g.ldr = H;
+    g.ws = ws + f.W.skws;
+    g.ws_bytes = f.W.skws_bytes;
     MK_RUN(launch_gemm_skinny(g, st));
   }
   MK_RUN(launch_rmsnorm_bf16(xl, H, nullptr, xnl, H, B, H, c.eps, st));
@@ -593,6 +600,8 @@ int launch_forward(const Fwd& f, hipStream_t st) {
     g.ldb = H;
     g.out = gul + (size_t)b0 * 2 * I;
     g.ldo = 2 * I;
+    g.ws = ws + f.W.skws;
+    g.ws_bytes = f.W.skws_bytes;
     MK_RUN(launch_gemm_skinny(g, st));
   }
   MK_RUN(launch_silu_mul_bf16(gul, hl, B, I, st));
@@ -610,6 +619,8 @@ int launch_forward(const Fwd& f, hipStream_t st) {
     g.epi = Epi::RES_BF16ADD;
     g.res = xl + (size_t)b0 * H;
     g.ldr = H;
+    g.ws = ws + f.W.skws;
+    g.ws_bytes = f.W.skws_bytes;
     MK_RUN(launch_gemm_skinny(g, st));
   }
   // ---- final norm into the (max(8, B), H) output, pad rows zero (mk_jax.py:569, :608-612)

@@ -25,7 +25,7 @@ struct PackedLayout {
 
 // Byte offsets of the forward's buffers inside the caller's workspace.
 struct WorkLayout {
-  size_t x, xq, sx, qkv, attn, xn, h, att, part, xnl, ql, attl, xl, gul, hl, total;
+  size_t x, xq, sx, qkv, attn, xn, h, att, part, xnl, ql, attl, xl, gul, hl, skws, skws_bytes, total;
 };
 
 struct GraphKey {
