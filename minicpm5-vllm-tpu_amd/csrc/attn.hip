@@ -37,31 +37,50 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(const uint16_t* __restri
                                                         uint16_t* __restrict__ krope,
                                                         uint16_t* __restrict__ vt, int S, int n_q,
                                                         int n_kv) {
-  __shared__ uint16_t vs[64][HD + 2];
-  const int t0 = blockIdx.x * 64, kv = blockIdx.y, b = blockIdx.z;
+  // 64 tokens of one kv head; 16-byte loads and stores throughout.  V goes through LDS for the
+  // transpose (row of 64 tokens + 8 pad elements: the column reads of 8 consecutive tokens spread
+  // over the banks).
+  constexpr int VR = 64 + 8;
+  __shared__ __attribute__((aligned(16))) uint16_t vs[HD][VR];
+  const int t0 = blockIdx.x * 64, kv = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
   const int D = (n_q + 2 * n_kv) * HD;
   const uint16_t* base = qkv + ((size_t)b * S + t0) * D;
-  constexpr int H2 = HD / 2;
+  constexpr int H2 = HD / 2, NC = HD / 16;   // 16-byte chunks per half row
   uint16_t* kdst = krope + (((size_t)b * n_kv + kv) * S + t0) * HD;
-  for (int idx = threadIdx.x; idx < 64 * H2; idx += 256) {
-    const int t = idx / H2, d = idx % H2;
+  for (int idx = tid; idx < 64 * NC; idx += 256) {
+    const int t = idx / NC, c = idx % NC;
     const uint16_t* kr = base + (size_t)t * D + (n_q + kv) * HD;
-    const float x1 = bf2f(kr[d]), x2 = bf2f(kr[d + H2]);
     const size_t tb = (size_t)(t0 + t) * HD;
-    const float c1 = bf2f(cosr[tb + d]), s1 = bf2f(sinr[tb + d]);
-    const float c2 = bf2f(cosr[tb + d + H2]), s2 = bf2f(sinr[tb + d + H2]);
-    kdst[(size_t)t * HD + d] = f2bf(x1 * c1 - x2 * s1);
-    kdst[(size_t)t * HD + d + H2] = f2bf(x2 * c2 + x1 * s2);
+    const u32x4 lo = *reinterpret_cast<const u32x4*>(kr + 8 * c);
+    const u32x4 hi = *reinterpret_cast<const u32x4*>(kr + H2 + 8 * c);
+    const u32x4 cl = *reinterpret_cast<const u32x4*>(cosr + tb + 8 * c);
+    const u32x4 ch = *reinterpret_cast<const u32x4*>(cosr + tb + H2 + 8 * c);
+    const u32x4 sl = *reinterpret_cast<const u32x4*>(sinr + tb + 8 * c);
+    const u32x4 sh = *reinterpret_cast<const u32x4*>(sinr + tb + H2 + 8 * c);
+    u32x4 olo, ohi;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float x1a = bf_lo(lo[e]), x1b = bf_hi(lo[e]), x2a = bf_lo(hi[e]), x2b = bf_hi(hi[e]);
+      olo[e] = pack_bf2(x1a * bf_lo(cl[e]) - x2a * bf_lo(sl[e]), x1b * bf_hi(cl[e]) - x2b * bf_hi(sl[e]));
+      ohi[e] = pack_bf2(x2a * bf_lo(ch[e]) + x1a * bf_lo(sh[e]), x2b * bf_hi(ch[e]) + x1b * bf_hi(sh[e]));
+    }
+    *reinterpret_cast<u32x4*>(kdst + (size_t)t * HD + 8 * c) = olo;
+    *reinterpret_cast<u32x4*>(kdst + (size_t)t * HD + H2 + 8 * c) = ohi;
   }
-  for (int idx = threadIdx.x; idx < 64 * HD; idx += 256) {
-    const int t = idx / HD, d = idx % HD;
-    vs[t][d] = base[(size_t)t * D + (n_q + n_kv + kv) * HD + d];
+  for (int idx = tid; idx < 64 * (HD / 8); idx += 256) {
+    const int t = idx / (HD / 8), c = idx % (HD / 8);
+    const u32x4 v = *reinterpret_cast<const u32x4*>(base + (size_t)t * D + (n_q + n_kv + kv) * HD + 8 * c);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      vs[8 * c + 2 * e][t] = (uint16_t)(v[e] & 0xffffu);
+      vs[8 * c + 2 * e + 1][t] = (uint16_t)(v[e] >> 16);
+    }
   }
   __syncthreads();
   uint16_t* vdst = vt + ((size_t)b * n_kv + kv) * HD * S + t0;
-  for (int idx = threadIdx.x; idx < 64 * HD; idx += 256) {
-    const int d = idx / 64, t = idx % 64;
-    vdst[(size_t)d * S + t] = vs[t][d];
+  for (int idx = tid; idx < HD * 8; idx += 256) {
+    const int d = idx / 8, c = idx % 8;
+    *reinterpret_cast<u32x4*>(vdst + (size_t)d * S + 8 * c) = *reinterpret_cast<const u32x4*>(&vs[d][8 * c]);
   }
 }
 
