@@ -8,15 +8,30 @@ namespace mk {
 
 namespace {
 
+// Wave reductions on the VALU: DPP lane permutes inside each row of 16 lanes (quad swaps, half-row
+// and row mirrors), then the four row results read as scalars -- no LDS round trips.  The order of
+// the operations is fixed, so a row's result is reproducible.
+template <int CTRL>
+__device__ inline float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+template <class Op>
+__device__ inline float wave_reduce(float v, Op op) {
+  v = op(v, dpp<0xb1>(v));    // quad_perm [1, 0, 3, 2]
+  v = op(v, dpp<0x4e>(v));    // quad_perm [2, 3, 0, 1]
+  v = op(v, dpp<0x141>(v));   // row_half_mirror: the other quad of the 8-lane half row
+  v = op(v, dpp<0x140>(v));   // row_mirror: the other half of the 16-lane row
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return op(op(r0, r1), op(r2, r3));
+}
 __device__ inline float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  return wave_reduce(v, [](float a, float b) { return a + b; });
 }
 __device__ inline float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  return wave_reduce(v, [](float a, float b) { return fmaxf(a, b); });
 }
 
 template <bool F32>
