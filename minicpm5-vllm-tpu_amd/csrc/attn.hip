@@ -558,27 +558,64 @@ __global__ __launch_bounds__(256) void last_attn_part_kernel(LastAttnArgs a) {
   }
 }
 
+// Merge of the chunk partials of one (head, sequence): M = max m_c, e_c = exp(m_c - M),
+// l = sum l_c e_c, o = sum o_c e_c; out = bf16(o / l).  256 threads: the chunks are split over
+// the threads in a fixed pattern and the partial sums combined in a fixed order.
+constexpr int MERGE_T = 256, MAX_CHUNKS = 2048;
+
 template <int HD>
-__global__ void last_attn_merge_kernel(LastAttnArgs a) {
-  const int head = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+__global__ __launch_bounds__(MERGE_T) void last_attn_merge_kernel(LastAttnArgs a) {
+  __shared__ float ec[MAX_CHUNKS];
+  __shared__ float red[MERGE_T / 64];
+  __shared__ float osum[MERGE_T / HD + 1][HD];
+  const int head = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int nchunk = a.S / LCH;
   const float* pp = a.part + ((size_t)b * a.n_q + head) * nchunk * (HD + 2);
-  float M = -INFINITY;
-  for (int c = 0; c < nchunk; ++c) M = fmaxf(M, pp[(size_t)c * (HD + 2)]);
-  float l = 0.f, o = 0.f;
-  for (int c = 0; c < nchunk; ++c) {
+  float mx = -INFINITY;
+  for (int c = tid; c < nchunk; c += MERGE_T) mx = fmaxf(mx, pp[(size_t)c * (HD + 2)]);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  if (lane == 0) red[w] = mx;
+  __syncthreads();
+  float M = red[0];
+#pragma unroll
+  for (int i = 1; i < MERGE_T / 64; ++i) M = fmaxf(M, red[i]);
+  __syncthreads();
+  float l = 0.f;
+  for (int c = tid; c < nchunk; c += MERGE_T) {
     const float e = __expf(pp[(size_t)c * (HD + 2)] - M);
+    ec[c] = e;
     l += pp[(size_t)c * (HD + 2) + 1] * e;
-    o += pp[(size_t)c * (HD + 2) + 2 + d] * e;
   }
-  a.out[((size_t)b * a.n_q + head) * HD + d] = f2bf(o / l);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) l += __shfl_xor(l, o, 64);
+  if (lane == 0) red[w] = l;
+  __syncthreads();
+  float L = 0.f;
+#pragma unroll
+  for (int i = 0; i < MERGE_T / 64; ++i) L += red[i];
+  // o: thread = (d, group g of chunks c = g, g + NG, ...), NG = threads per d
+  constexpr int NG = MERGE_T / HD;
+  if (tid < NG * HD) {
+    const int d = tid % HD, g = tid / HD;
+    float o = 0.f;
+    for (int c = g; c < nchunk; c += NG) o += pp[(size_t)c * (HD + 2) + 2 + d] * ec[c];
+    osum[g][d] = o;
+  }
+  __syncthreads();
+  if (tid < HD) {
+    float o = 0.f;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) o += osum[g][tid];
+    a.out[((size_t)b * a.n_q + head) * HD + tid] = f2bf(o / L);
+  }
 }
 
 template <int HD>
 int launch_last_attn_hd(const LastAttnArgs& a, hipStream_t st) {
   hipLaunchKernelGGL(last_attn_part_kernel<HD>, dim3(a.S / LCH, a.n_kv, a.B), dim3(256), 0, st, a);
   MK_HIP_CHECK(hipGetLastError());
-  hipLaunchKernelGGL(last_attn_merge_kernel<HD>, dim3(a.n_q, a.B), dim3(HD), 0, st, a);
+  hipLaunchKernelGGL(last_attn_merge_kernel<HD>, dim3(a.n_q, a.B), dim3(MERGE_T), 0, st, a);
   MK_HIP_CHECK(hipGetLastError());
   return MK_OK;
 }
@@ -618,6 +655,7 @@ int launch_last_attn(const LastAttnArgs& a, hipStream_t st) {
   int rc = attn_validate(a.B, a.S, a.n_q, a.n_kv, a.hd);
   if (rc) return rc;
   MK_REQUIRE(a.S % LCH == 0, "last-token attention: seq must be a multiple of 64");
+  MK_REQUIRE(a.S / LCH <= MAX_CHUNKS, "last-token attention: seq must be <= 131072");
   switch (a.hd) {
     case 64: return launch_last_attn_hd<64>(a, st);
     case 96: return launch_last_attn_hd<96>(a, st);
