@@ -40,12 +40,19 @@ struct GemmCfg {
   static constexpr int WM = BM / WGM, WN = BN / WGN;     // wave tile
   static constexpr int MT = WM / 32, NTL = WN / 32;       // 32x32 MFMA tiles per wave
   static constexpr int A_BYTES = BM * BKB, ST_BYTES = (BM + BN) * BKB;
-  static constexpr int AQ = BM / 16 / NW, BQ = BN / 16 / NW;   // 1 KB async-load instructions per wave
+  // a stage is NL blocks of 16 rows x 64 bytes (1 KB, one async-load instruction): A blocks 0 .. NA-1,
+  // then B blocks; block b is loaded by wave b % NW.  Waves w < NL % NW load QH blocks, the rest QL.
+  static constexpr int NA = BM / 16, NL = (BM + BN) / 16;
+  static constexpr int QL = NL / NW, QH = (NL + NW - 1) / NW, NQH = NL % NW == 0 ? NW : NL % NW;
   static constexpr int EROW = WN * 4 + 16;                // epilogue LDS row (f32 + pad)
-  static_assert(BM % (16 * NW) == 0 && BN % (16 * NW) == 0, "load split");
+  static_assert(BM % 16 == 0 && BN % 16 == 0 && NA % NW == 0, "load split: A blocks evenly over the waves");
+  static_assert(LOOP == 1 || NL % NW == 0, "split k-step loop: the same load count on every wave");
   static_assert(NW * 32 * EROW <= NST * ST_BYTES, "epilogue staging fits in the ring");
-  static_assert(WN % 64 == 0 || WN == 32, "wave tile width");
-  static_assert(LOOP == 0 || (WGM == 2 && NST >= 3), "ping-pong needs two wave groups and two stages in flight");
+  static_assert(WN % 32 == 0, "wave tile width");
+  // ping-pong: waves w and w + 4 share a SIMD and belong to groups 0 and 1; each group loads a uniform
+  // number of blocks per stage
+  static_assert(LOOP == 0 || (NW == 8 && NST >= 3 && NQH % 4 == 0),
+                "ping-pong needs two groups of four waves with uniform loads and two stages in flight");
 };
 // 256x256 block, 128x128 per wave (accumulators in AGPRs), one workgroup per CU
 using CfgL = GemmCfg<256, 256, 2, 2, 3, 1, 0>;
@@ -55,6 +62,9 @@ using CfgM = GemmCfg<256, 128, 2, 2, 3, 2>;
 using CfgS = GemmCfg<128, 128, 2, 2, 3, 3>;
 // 256x256 block, 8 waves of 128x64 (two per SIMD), one workgroup per CU
 using CfgX = GemmCfg<256, 256, 2, 4, 4, 1, 1>;
+// 256x192 block, 8 waves of 64x96 (two per SIMD), one workgroup per CU: N = 1536 in 8 column tiles, so
+// M = 8192 fills exactly 256 CUs
+using CfgN = GemmCfg<256, 192, 4, 2, 4, 1, 1>;
 
 template <GemmIn IN>
 struct Mma;
@@ -171,29 +181,52 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
   const int m0 = (first_m + wig % gsz) * C::BM, n0 = (wig / gsz) * C::BN;
   const int lda = g.lda * T::ESZ, ldb = g.ldb * T::ESZ;   // bytes
   const int Kb = g.K * T::ESZ;
-  constexpr int Q = C::AQ + C::BQ;                        // async-load instructions per wave per stage
+  // async-load instructions per wave per stage: QH on waves w < NQH (ping-pong group 0 when uneven)
+  constexpr int Q = C::QH;
+  const bool qfull = C::QH == C::QL || w < C::NQH;
 
-  // this lane's async-load sources: rows 16 q + lane / 4 of A (q = AQ w + j) and B (q = BQ w + j) as
+  // this lane's async-load sources: block b = w + NW j, rows 16 (b or b - NA) + lane / 4 of A or B, as
   // 32-bit byte offsets from the operand base (the base and the K offset stay scalar); rows past M / N
   // are clamped (their results are never stored)
-  uint32_t aoff[C::AQ], boff[C::BQ];
+  constexpr int JA = C::NA / C::NW;                       // load instructions j < JA are A blocks
+  uint32_t loff[Q];
 #pragma unroll
-  for (int j = 0; j < C::AQ; ++j) {
-    const int r = 16 * (C::AQ * w + j) + (lane >> 2);
-    aoff[j] = (uint32_t)min(m0 + r, g.M - 1) * (uint32_t)lda + 16u * ((lane & 3) ^ swz(r));
-  }
-#pragma unroll
-  for (int j = 0; j < C::BQ; ++j) {
-    const int r = 16 * (C::BQ * w + j) + (lane >> 2);
-    boff[j] = (uint32_t)min(n0 + r, g.N - 1) * (uint32_t)ldb + 16u * ((lane & 3) ^ swz(r));
+  for (int j = 0; j < Q; ++j) {
+    const int b = w + C::NW * j;
+    if (j < JA) {
+      const int r = 16 * b + (lane >> 2);
+      loff[j] = (uint32_t)min(m0 + r, g.M - 1) * (uint32_t)lda + 16u * ((lane & 3) ^ swz(r));
+    } else {
+      const int r = 16 * (b - C::NA) + (lane >> 2);
+      loff[j] = (uint32_t)min(n0 + r, g.N - 1) * (uint32_t)ldb + 16u * ((lane & 3) ^ swz(r));
+    }
   }
   const char* const Ag = static_cast<const char*>(g.A);
   const char* const Bg = static_cast<const char*>(g.B);
-  // async load j (of Q) of stage `st` at K byte offset kb
+  // async load j (of Q) of stage `st` at K byte offset kb; block b sits at b KB in the stage (A blocks,
+  // then B blocks)
   auto issue1 = [&](int j, int st, int kb) {
-    char* base = smem + st * C::ST_BYTES;
-    if (j < C::AQ) copy16_to_lds(Ag + kb + aoff[j], base + (C::AQ * w + j) * 1024);
-    else copy16_to_lds(Bg + kb + boff[j - C::AQ], base + C::A_BYTES + (C::BQ * w + j - C::AQ) * 1024);
+    char* dst = smem + st * C::ST_BYTES + (w + C::NW * j) * 1024;
+    if (j < JA) copy16_to_lds(Ag + kb + loff[j], dst);
+    else if (j < C::QL || qfull) copy16_to_lds(Bg + kb + loff[j], dst);
+  };
+  // wait until at most `n` stages of this wave's async loads are outstanding
+  auto wait_stages = [&](int n) {
+    if (C::QH == C::QL || qfull) {
+      switch (n) {
+        case 0: MK_WAIT_VMCNT(0); break;
+        case 1: MK_WAIT_VMCNT(C::QH); break;
+        case 2: MK_WAIT_VMCNT(2 * C::QH); break;
+        default: MK_WAIT_VMCNT(3 * C::QH); break;
+      }
+    } else {
+      switch (n) {
+        case 0: MK_WAIT_VMCNT(0); break;
+        case 1: MK_WAIT_VMCNT(C::QL); break;
+        case 2: MK_WAIT_VMCNT(2 * C::QL); break;
+        default: MK_WAIT_VMCNT(3 * C::QL); break;
+      }
+    }
   };
 
   Acc acc[C::MT][C::NTL];
@@ -235,7 +268,10 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
   constexpr bool DQ = EPI == Epi::DQ_BF16 || EPI == Epi::DQ2_BF16 || EPI == Epi::DQ_RES_BF16ADD ||
                       EPI == Epi::DQ2_RES_F32ADD || EPI == Epi::DQ2_RES_BF16ADD || EPI == Epi::DQ_SILU ||
                       EPI == Epi::DQ_SILU_F32A || EPI == Epi::SILU_BF16;   // SILU_BF16: only with scales
-  constexpr int TPR = SILU ? C::WN / 16 : C::WN / 8;   // tasks per row
+  // wave tiles whose width is not a multiple of 64 are processed in 32-column passes
+  constexpr int EW = (SILU || C::WN % 64 == 0) ? C::WN : 32;
+  constexpr int NSB = C::WN / EW;
+  constexpr int TPR = SILU ? EW / 16 : EW / 8;         // tasks per row
   constexpr int TRS = 64 / TPR;                        // rows between a lane's tasks
   constexpr int NTASK = 32 / TRS;
   static_assert(64 % TPR == 0 && 32 % TRS == 0, "epilogue task split");
@@ -244,20 +280,24 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
   const int nb0 = n0 + wn * C::WN;                     // first column of the wave
   // SiLU: 64-column block blk of the wave is [32 gate | 32 up]; this lane's gate columns start at pg
   const int pg = SILU ? min(nb0 + (tcol >> 2) * 64, g.N - 64) + (tcol & 3) * 8 : 0;
-  const int pc = SILU ? pg : min(nb0 + tcol * 8, g.N - 8);
+  auto pcol = [&](int sb) { return SILU ? pg : min(nb0 + sb * EW + tcol * 8, g.N - 8); };
   const bool dq = DQ && g.rs != nullptr;
   float rsv[C::MT][NTASK];
-  f32x4 csv[SILU ? 4 : 2];
+  f32x4 csv[NSB][SILU ? 4 : 2];
   if (dq) {
 #pragma unroll
     for (int mt = 0; mt < C::MT; ++mt)
 #pragma unroll
       for (int i = 0; i < NTASK; ++i) rsv[mt][i] = g.rs[min(m0 + wm * C::WM + mt * 32 + trow0 + i * TRS, g.M - 1)];
-    csv[0] = *reinterpret_cast<const f32x4*>(g.cs + pc);
-    csv[1] = *reinterpret_cast<const f32x4*>(g.cs + pc + 4);
-    if constexpr (SILU) {
-      csv[2] = *reinterpret_cast<const f32x4*>(g.cs + pc + 32);
-      csv[3] = *reinterpret_cast<const f32x4*>(g.cs + pc + 36);
+#pragma unroll
+    for (int sb = 0; sb < NSB; ++sb) {
+      const int pc = pcol(sb);
+      csv[sb][0] = *reinterpret_cast<const f32x4*>(g.cs + pc);
+      csv[sb][1] = *reinterpret_cast<const f32x4*>(g.cs + pc + 4);
+      if constexpr (SILU) {
+        csv[sb][2] = *reinterpret_cast<const f32x4*>(g.cs + pc + 32);
+        csv[sb][3] = *reinterpret_cast<const f32x4*>(g.cs + pc + 36);
+      }
     }
   }
 
@@ -268,8 +308,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int j = 0; j < Q; ++j) issue1(j, s0, s0 * BKB);
     }
-  if (nk >= C::NST - 1) MK_WAIT_VMCNT((C::NST - 2) * Q);
-  else MK_WAIT_VMCNT(0);
+  if (nk >= C::NST - 1) wait_stages(C::NST - 2);
+  else wait_stages(0);
   lds_barrier();
   // Materialize the epilogue's kernel arguments now: a scalar load still pending inside the loop would
   // turn every LDS wait there into lgkmcnt(0) (scalar loads return out of order).
@@ -297,15 +337,18 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
       acc[mt][nt] = T::run(src[C::NTL + mt], src[nt], acc[mt][nt]);
     };
     // stages 0 and 1 visible; stage 0 in H0 / H1
-    if (nk >= D) MK_WAIT_VMCNT((D - 2) * Q);
-    else MK_WAIT_VMCNT(0);
+    if (nk >= D) wait_stages(D - 2);
+    else wait_stages(0);
     lds_barrier();
 #pragma unroll
     for (int q = 0; q < NOP; ++q) rdq(smem, 0, q, H0);
 #pragma unroll
     for (int q = 0; q < NOP; ++q) rdq(smem, 1, q, H1);
     __builtin_amdgcn_s_waitcnt(0xc07f);
-    if (wm == 1) lds_barrier();
+    // ping-pong group of this wave: waves w and w + 4 share a SIMD; group 0 loads QH blocks per stage,
+    // group 1 QL
+    const int wgrp = w >> 2;
+    if (wgrp == 1) lds_barrier();
     int cur = 0;
     // `steady` instances (stage it + D exists) have no runtime conditions, so the compute phase stays one
     // basic block instead of a branch around every operand read
@@ -318,8 +361,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
 #pragma unroll
         for (int j = 0; j < Q; ++j) issue1(j, nslot, (it + D) * BKB);
       }
-      if (wm == 0 && (ST || it + 1 < nk)) {
-        if (pre) MK_WAIT_VMCNT((D - 1) * Q);
+      if (wgrp == 0 && (ST || it + 1 < nk)) {
+        if (pre) MK_WAIT_VMCNT((D - 1) * C::QH);
         else MK_WAIT_VMCNT(0);
       }
       lds_barrier();
@@ -348,8 +391,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
         if (nxt) rdq(S1, 1, q, ha);
       __builtin_amdgcn_s_setprio(0);
       __builtin_amdgcn_s_waitcnt(0xc07f);                 // lgkmcnt(0): stage it + 1 is in registers
-      if (wm == 1 && (ST || it + 2 < nk)) {
-        if (pre) MK_WAIT_VMCNT((D - 2) * Q);
+      if (wgrp == 1 && (ST || it + 2 < nk)) {
+        if (pre) MK_WAIT_VMCNT((D - 2) * C::QL);
         else MK_WAIT_VMCNT(0);
       }
       lds_barrier();
@@ -368,7 +411,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
       if (it + 1 < nk) step(Tail{}, it + 1, H2, H0, H1);
       if (it + 2 < nk) step(Tail{}, it + 2, H1, H2, H0);
     }
-    if (wm == 0) lds_barrier();
+    if (wgrp == 0) lds_barrier();
   } else {
     u32x4 ra0[C::MT], rb0[C::NTL], ra1[C::MT], rb1[C::NTL];
     rd(smem, ao0, bo0, ra0, rb0);
@@ -420,13 +463,15 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
   // column, 16 rows); each 32-row slice of the wave's tile is written to the wave's own LDS region,
   // then every lane handles 8 consecutive columns of a row with 16-byte accesses.  The residual rows of
   // slice mt + 1 are loaded while slice mt is processed.
-  u32x4 rv[2][NTASK];
-  auto load_res = [&](int mt, u32x4 (&dst)[NTASK]) {
+  u32x4 rv[2][NSB][NTASK];
+  auto load_res = [&](int mt, u32x4 (&dst)[NSB][NTASK]) {
 #pragma unroll
-    for (int i = 0; i < NTASK; ++i) {
-      const int m = min(m0 + wm * C::WM + mt * 32 + trow0 + i * TRS, g.M - 1);
-      dst[i] = *reinterpret_cast<const u32x4*>(g.res + (size_t)m * g.ldr + pc);
-    }
+    for (int sb = 0; sb < NSB; ++sb)
+#pragma unroll
+      for (int i = 0; i < NTASK; ++i) {
+        const int m = min(m0 + wm * C::WM + mt * 32 + trow0 + i * TRS, g.M - 1);
+        dst[sb][i] = *reinterpret_cast<const u32x4*>(g.res + (size_t)m * g.ldr + pcol(sb));
+      }
   };
   if constexpr (RES) load_res(0, rv[0]);
   lds_barrier();   // every wave is done reading the LDS ring
@@ -463,8 +508,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
         for (int e = 0; e < 8; ++e) {
           const float gacc = T::f(e < 4 ? g0[e] : g1[e - 4]);
           const float uacc = T::f(e < 4 ? u0[e] : u1[e - 4]);
-          const float sg = dq ? csv[e >> 2][e & 3] : 1.f;
-          const float su = dq ? csv[2 + (e >> 2)][e & 3] : 1.f;
+          const float sg = dq ? csv[0][e >> 2][e & 3] : 1.f;
+          const float su = dq ? csv[0][2 + (e >> 2)][e & 3] : 1.f;
           const float rs = dq ? rsv[mt][i] : 1.f;
           if constexpr (EPI == Epi::SILU_BF16) {
             // XLA path (mk_jax.py:283-299, :420-421): gu rounded to bf16, silu and product in bf16
@@ -492,9 +537,11 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
         }
       }
     } else {
-      const int c8 = tcol * 8, n = nb0 + c8;
+#pragma unroll
+      for (int sb = 0; sb < NSB; ++sb)
 #pragma unroll
       for (int i = 0; i < NTASK; ++i) {
+        const int c8 = sb * EW + tcol * 8, n = nb0 + c8;
         const int lr = trow0 + i * TRS, m = mrow0 + lr;
         const V4* vp = reinterpret_cast<const V4*>(er + lr * EROW + c8 * 4);
         const V4 r0 = vp[0], r1 = vp[1];
@@ -520,7 +567,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
         if constexpr (DQ) {
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
-            const float cs = csv[e >> 2][e & 3];
+            const float cs = csv[sb][e >> 2][e & 3];
             if constexpr (EPI == Epi::DQ2_BF16 || EPI == Epi::DQ2_RES_F32ADD || EPI == Epi::DQ2_RES_BF16ADD)
               v[e] = v[e] * (rsv[mt][i] * cs);
             else v[e] = (v[e] * rsv[mt][i]) * cs;
@@ -531,7 +578,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
         for (int e = 0; e < 4; ++e) {
           float a = v[2 * e], b = v[2 * e + 1];
           if constexpr (RES) {
-            const float ra = bf_lo(rv[mt & 1][i][e]), rb = bf_hi(rv[mt & 1][i][e]);
+            const float ra = bf_lo(rv[mt & 1][sb][i][e]), rb = bf_hi(rv[mt & 1][sb][i][e]);
             if constexpr (EPI == Epi::RES_BF16ADD || EPI == Epi::DQ_RES_BF16ADD || EPI == Epi::DQ2_RES_BF16ADD) {
               a = ra + bf2f(f2bf(a));
               b = rb + bf2f(f2bf(b));
@@ -625,20 +672,20 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(GemmArgs g, int spli
 // per tile, except for the SiLU epilogue, whose VALU work is hidden better by two co-resident
 // 256x128 workgroups.
 int choose_cfg(const GemmArgs& g) {
-  if (g.cfg >= 1 && g.cfg <= 4) return g.cfg;
+  const bool silu = g.epi == Epi::DQ_SILU || g.epi == Epi::DQ_SILU_F32A || g.epi == Epi::SILU_BF16;
+  if (g.cfg >= 1 && g.cfg <= 5 && !(silu && g.cfg == 5)) return g.cfg;
   static const int forced = [] {
-    const char* e = std::getenv("MK_GEMM_CFG");   // tuning override: 1 .. 4
+    const char* e = std::getenv("MK_GEMM_CFG");   // tuning override: 1 .. 5
     return e ? std::atoi(e) : 0;
   }();
-  if (forced >= 1 && forced <= 4) return forced;
-  const bool silu = g.epi == Epi::DQ_SILU || g.epi == Epi::DQ_SILU_F32A || g.epi == Epi::SILU_BF16;
+  if (forced >= 1 && forced <= 5 && !(silu && forced == 5)) return forced;
   struct Opt { int id, bm, bn; double eff; };
-  const Opt opts[4] = {{4, 256, 256, silu ? 1.05 : 1.25}, {2, 256, 128, 1.0}, {1, 256, 256, 0.9},
-                       {3, 128, 128, 0.85}};
+  const Opt opts[5] = {{4, 256, 256, silu ? 1.05 : 1.25}, {2, 256, 128, 1.0}, {1, 256, 256, 0.9},
+                       {3, 128, 128, 0.85}, {5, 256, 192, 1.15}};
   int best = 2;
   double bt = 1e300;
   for (const Opt& o : opts) {
-    if (silu && o.id == 3) continue;                 // 64-column waves: fine, but never faster
+    if (silu && (o.id == 3 || o.id == 5)) continue;   // 3: never faster; 5: 96-column waves (no SiLU)
     const double tiles = (double)((g.M + o.bm - 1) / o.bm) * ((g.N + o.bn - 1) / o.bn);
     const double t = std::ceil(tiles / 256.0) * o.bm * o.bn / o.eff;
     if (t < bt * 0.999) {
@@ -671,6 +718,13 @@ void launch_t(const GemmArgs& g, hipStream_t st) {
     case 1: launch_c<CfgL, IN, EPI>(g, st); break;
     case 3: launch_c<CfgS, IN, EPI>(g, st); break;
     case 4: launch_c<CfgX, IN, EPI>(g, st); break;
+    case 5:
+      if constexpr (EPI != Epi::DQ_SILU && EPI != Epi::DQ_SILU_F32A && EPI != Epi::SILU_BF16) {
+        launch_c<CfgN, IN, EPI>(g, st);
+        break;
+      }
+      launch_c<CfgM, IN, EPI>(g, st);
+      break;
     default: launch_c<CfgM, IN, EPI>(g, st); break;
   }
 }
