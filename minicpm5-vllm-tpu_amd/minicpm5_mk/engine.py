@@ -17,6 +17,7 @@ and run through libmk (`MkModel`).
 from __future__ import annotations
 
 import dataclasses
+import os
 import time
 from dataclasses import dataclass, field
 
@@ -108,6 +109,9 @@ class MkEngine:
     def __init__(self, model="1b", quant: str = "auto", state_dict: dict | None = None, weight_seed: int = 0,
                  max_model_len: int = 8256, device: str = "cuda:0", log=print):
         t0 = time.perf_counter()
+        if isinstance(model, str) and os.path.isdir(model):   # local HF checkpoint directory
+            from .checkpoint import load_local_checkpoint
+            model, state_dict = load_local_checkpoint(model)
         self.cfg = preset(model) if isinstance(model, str) else model
         self.cfg.validate()
         cfg = self.cfg
