@@ -91,7 +91,9 @@ struct AttnSmem {
                                              // of 8 consecutive rows hit distinct banks
   static constexpr int KBYTES = KT * KROW;
   static constexpr int VBYTES = HD * VROW;
-  static constexpr int NK = 3, NV = 2;       // K ring (QK runs one tile ahead), V ring
+  // K and V rings of 4 slots: a step stores K three tiles and V two tiles ahead, so the workgroup
+  // barrier is needed only every second step
+  static constexpr int NK = 4, NV = 4;
   static constexpr int TOTAL = NK * KBYTES + NV * VBYTES;
   static constexpr int KCH = KT * HD / 8;    // 16-byte chunks per K tile
   static constexpr int VCH = HD * KT / 8;    // 16-byte chunks per V^T tile
@@ -148,7 +150,7 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
   const uint16_t* vg = vt + ((size_t)b * n_kv + kv) * (size_t)HD * S;
 
   u32x4 kst[L::KPT], vst[L::VPT];
-  auto gload_k = [&](int kt) {
+  auto gload_k = [&](int kt, u32x4 (&kst)[L::KPT]) {
 #pragma unroll
     for (int i = 0; i < L::KPT; ++i) {
       const int c = tid + i * NT;
@@ -158,7 +160,7 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
       }
     }
   };
-  auto gload_v = [&](int kt) {
+  auto gload_v = [&](int kt, u32x4 (&vst)[L::VPT]) {
 #pragma unroll
     for (int i = 0; i < L::VPT; ++i) {
       const int c = tid + i * NT;
@@ -168,7 +170,7 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
       }
     }
   };
-  auto sstore_k = [&](int slot) {
+  auto sstore_k = [&](int slot, const u32x4 (&kst)[L::KPT]) {
     char* ks = kring + slot * L::KBYTES;
 #pragma unroll
     for (int i = 0; i < L::KPT; ++i) {
@@ -179,7 +181,7 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
       }
     }
   };
-  auto sstore_v = [&](int slot) {
+  auto sstore_v = [&](int slot, const u32x4 (&vst)[L::VPT]) {
     char* vs = vring + slot * L::VBYTES;
 #pragma unroll
     for (int i = 0; i < L::VPT; ++i) {
@@ -300,23 +302,30 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
       l += psum;
     };
 
-    // ---- prologue: K(0), V(0), K(1) staged; S(0) computed
+    // ---- prologue: K(0..2), V(0..1) staged (indices clamped to the last tile); S(0) computed
     __syncthreads();   // the previous pass (output staging) is done with the LDS
-    gload_k(0);
-    gload_v(0);
-    sstore_k(0);
-    sstore_v(0);
-    if (nkt > 1) {
-      gload_k(1);
-      sstore_k(1);
+    {
+      u32x4 k1[L::KPT], k2[L::KPT], v1[L::VPT];
+      gload_k(0, kst);
+      gload_v(0, vst);
+      gload_k(min(1, nkt - 1), k1);
+      gload_v(min(1, nkt - 1), v1);
+      gload_k(min(2, nkt - 1), k2);
+      sstore_k(0, kst);
+      sstore_v(0, vst);
+      sstore_k(1, k1);
+      sstore_v(1, v1);
+      sstore_k(2, k2);
     }
     __syncthreads();
     f32x16 scur[2], snext[2];
     qk(0, scur);
     rowmax_rescale(0, scur);
 
-    // ---- steady state: step t computes QK(t+1), softmax + PV(t) and stages K(t+2), V(t+1).
-    // The two waves of a SIMD run in step (one barrier per tile), so a wave overlaps its own VALU
+    // ---- steady state: step t computes QK(t+1), softmax + PV(t) and stages K(t+3), V(t+2) into the
+    // slots K(t-1), V(t-2) left.  A workgroup barrier follows every odd step; between two barriers a wave
+    // is at most one step ahead of another, and the 4-slot rings keep the tiles that either step
+    // reads apart from the ones that either step writes.  The waves of a SIMD run together, so a wave overlaps its own VALU
     // work with its MFMAs: the QK(t+1) MFMAs are issued with the softmax of tile t (exp2, bf16 P,
     // row sum) interleaved, the PV(t) MFMAs with the row max of tile t+1 interleaved.  Each step is
     // one MFMA plus a slice of the VALU work; LDS operands are read PF steps ahead.  Only the last
@@ -324,8 +333,8 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
     constexpr int NQK = 2 * KS, NPV = 4 * DT, NCH = 16, PF = 3;
     auto step = [&](auto mask, int t, const f32x16 (&sc)[2], f32x16 (&sn)[2]) {
       constexpr bool MASK = decltype(mask)::value;
-      gload_k(min(t + 2, nkt - 1));   // the clamped reload at the end lands in a free slot
-      gload_v(t + 1);
+      gload_k(min(t + 3, nkt - 1), kst);   // clamped reloads at the end land in free slots
+      gload_v(min(t + 2, nkt - 1), vst);
       const char* ksl = kring + ((t + 1) % L::NK) * L::KBYTES;
       auto kread = [&](int j) {
         const int s = j / 2, c = j % 2;
@@ -380,10 +389,10 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
         for (int k = j * NCH / NPV; k < (j + 1) * NCH / NPV; ++k)
           mx = fmaxf(mx, fmaxf(sn[k / 8][2 * (k % 8)], sn[k / 8][2 * (k % 8) + 1]));
         if (j == NPV / 2) {
-          // K(t+2) and V(t+1) into the slots K(t-1) and V(t-1) left (read in steps t-2 and t-1): their
+          // K(t+3) and V(t+2) into the slots K(t-1) and V(t-2) left (last read in steps t-2): their
           // global loads were issued at the start of the step
-          sstore_k((t + 2) % L::NK);
-          sstore_v((t + 1) % L::NV);
+          sstore_k((t + 3) % L::NK, kst);
+          sstore_v((t + 2) % L::NV, vst);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -398,7 +407,7 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
         for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
         m = mnew;
       }
-      __syncthreads();
+      if (t & 1) __syncthreads();
     };
     using Plain = std::integral_constant<bool, false>;
     using Diag = std::integral_constant<bool, true>;
