@@ -102,6 +102,15 @@ struct AttnSmem {
   static_assert(G * QT * (HD * 2 + 16) <= TOTAL, "output staging must fit in the K/V rings");
 };
 
+// The softmax of a 64-key tile is done in 16 chunks (chunk k: keys 32 (k / 8) + 16 ((k / 4) % 2) + ...,
+// 4 bf16 pairs of P^T); the PV MFMAs j >= (k / 4) * DT use chunk k.  Chunks nqc.. are computed one per PV
+// MFMA (chunk k right after MFMA k - nqc): each must be done before the first MFMA that uses it.
+constexpr bool softmax_deadlines_ok(int nqc, int dt) {
+  for (int k = nqc; k < 16; ++k)
+    if (k - nqc > (k / 4) * dt - 1) return false;
+  return true;
+}
+
 // Online softmax keeps a per-row reference max m and rescales O / l only when a row max exceeds
 // it by more than RESCALE_T (log2 units): p = exp2(s - m) <= 2^8 stays exact in f32 and in bf16's
 // relative precision, and O / l is unchanged by the choice of m.
@@ -325,12 +334,16 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
     // ---- steady state: step t computes QK(t+1), softmax + PV(t) and stages K(t+3), V(t+2) into the
     // slots K(t-1), V(t-2) left.  A workgroup barrier follows every odd step; between two barriers a wave
     // is at most one step ahead of another, and the 4-slot rings keep the tiles that either step
-    // reads apart from the ones that either step writes.  The waves of a SIMD run together, so a wave overlaps its own VALU
-    // work with its MFMAs: the QK(t+1) MFMAs are issued with the softmax of tile t (exp2, bf16 P,
-    // row sum) interleaved, the PV(t) MFMAs with the row max of tile t+1 interleaved.  Each step is
-    // one MFMA plus a slice of the VALU work; LDS operands are read PF steps ahead.  Only the last
+    // reads apart from the ones that either step writes.  The waves of a SIMD run together, so a wave
+    // overlaps its own VALU work with its MFMAs, spread evenly over the step: the QK(t+1) MFMAs carry
+    // the softmax of keys 0..31 of tile t (exp2, bf16 P, row sum), the first half of the PV(t) MFMAs
+    // (which use those keys) the softmax of keys 32..63, the second half the row max of tile t+1.  Each
+    // MFMA is issued with a slice of the VALU work; LDS operands are read PF MFMAs ahead.  Only the last
     // key tile crosses the diagonal, so the causal mask lives in the MASK instance of the step alone.
     constexpr int NQK = 2 * KS, NPV = 4 * DT, NCH = 16, PF = 3;
+    constexpr int NQC = HD == 64 ? 12 : 8;   // softmax chunks computed in the QK loop
+    constexpr int NPC = NCH - NQC;           // the rest: one per PV MFMA, then the row max
+    static_assert(NPC < NPV && softmax_deadlines_ok(NQC, DT), "softmax chunks must be ready for their PV MFMAs");
     auto step = [&](auto mask, int t, const f32x16 (&sc)[2], f32x16 (&sn)[2]) {
       constexpr bool MASK = decltype(mask)::value;
       gload_k(min(t + 3, nkt - 1), kst);   // clamped reloads at the end land in free slots
@@ -343,6 +356,14 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
       u32x4 kr[NQK];
       u32x4 pb[2][2];
       float psum = 0.f;
+      // P chunk k (keys 32 c + 16 s2 + 4 half + {0..3, 8..11}, 2 e and 2 e + 1 of them): exp2, bf16, row sum
+      auto softmax_chunk = [&](const f32x16 (&sc)[2], int k) {
+        const int c = k / 8, s2 = (k / 4) % 2, e = k % 4;
+        const float p0 = fast_exp2(sc[c][8 * s2 + 2 * e] - m);
+        const float p1 = fast_exp2(sc[c][8 * s2 + 2 * e + 1] - m);
+        pb[c][s2][e] = pack_bf2(p0, p1);
+        psum = dot2_bf16_sum(pb[c][s2][e], psum);
+      };
       sn[0] = f32x16{};
       sn[1] = f32x16{};
 #pragma unroll
@@ -352,13 +373,7 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
         if (j + PF < NQK) kr[j + PF] = kread(j + PF);
         sn[j % 2] = mfma_bf16_32x32x16(kr[j], qreg[j / 2], sn[j % 2]);
 #pragma unroll
-        for (int k = j * NCH / NQK; k < (j + 1) * NCH / NQK; ++k) {
-          const int c = k / 8, s2 = (k / 4) % 2, e = k % 4;
-          const float p0 = fast_exp2(sc[c][8 * s2 + 2 * e] - m);
-          const float p1 = fast_exp2(sc[c][8 * s2 + 2 * e + 1] - m);
-          pb[c][s2][e] = pack_bf2(p0, p1);
-          psum = dot2_bf16_sum(pb[c][s2][e], psum);
-        }
+        for (int k = j * NQC / NQK; k < (j + 1) * NQC / NQK; ++k) softmax_chunk(sc, k);
         __builtin_amdgcn_sched_barrier(0);
       }
       if constexpr (MASK) {
@@ -385,9 +400,14 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
         if (j + PF < NPV) vr[j + PF] = vread(j + PF);
         const int c = j / (2 * DT), s2 = (j / DT) % 2, dt = j % DT;
         o[dt] = mfma_bf16_32x32x16(vr[j], pb[c][s2], o[dt]);
+        if (j < NPC) {
+          softmax_chunk(sc, NQC + j);
+        } else {
+          constexpr int NM = NPV - NPC;
 #pragma unroll
-        for (int k = j * NCH / NPV; k < (j + 1) * NCH / NPV; ++k)
-          mx = fmaxf(mx, fmaxf(sn[k / 8][2 * (k % 8)], sn[k / 8][2 * (k % 8) + 1]));
+          for (int k = (j - NPC) * NCH / NM; k < (j - NPC + 1) * NCH / NM; ++k)
+            mx = fmaxf(mx, fmaxf(sn[k / 8][2 * (k % 8)], sn[k / 8][2 * (k % 8) + 1]));
+        }
         if (j == NPV / 2) {
           // K(t+3) and V(t+2) into the slots K(t-1) and V(t-2) left (last read in steps t-2): their
           // global loads were issued at the start of the step
