@@ -432,10 +432,15 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
     using Plain = std::integral_constant<bool, false>;
     using Diag = std::integral_constant<bool, true>;
     int t = 0;
-    for (; t + 2 < nkt; ++t) {
+    for (; t + 3 < nkt; t += 2) {
+      step(Plain{}, t, scur, snext);
+      step(Plain{}, t + 1, snext, scur);
+    }
+    if (t + 2 < nkt) {
       step(Plain{}, t, scur, snext);
       scur[0] = snext[0];
       scur[1] = snext[1];
+      ++t;
     }
     if (t + 1 < nkt) {   // step nkt - 2: QK of the diagonal tile
       step(Diag{}, t, scur, snext);
