@@ -295,8 +295,8 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
           u32x4 pb;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const float p0 = fast_exp2(sacc[c][8 * s2 + 2 * e] - m);
-            const float p1 = fast_exp2(sacc[c][8 * s2 + 2 * e + 1] - m);
+            const float p0 = fast_exp2(sacc[c][8 * s2 + 2 * e]);
+            const float p1 = fast_exp2(sacc[c][8 * s2 + 2 * e + 1]);
             pb[e] = pack_bf2(p0, p1);
             psum = dot2_bf16_sum(pb[e], psum);
           }
@@ -330,6 +330,10 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
     f32x16 scur[2], snext[2];
     qk(0, scur);
     rowmax_rescale(0, scur);
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) scur[c][r] -= m;   // scores are kept relative to m from here on
 
     // ---- steady state: step t computes QK(t+1), softmax + PV(t) and stages K(t+3), V(t+2) into the
     // slots K(t-1), V(t-2) left.  A workgroup barrier follows every odd step; between two barriers a wave
@@ -359,13 +363,18 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
       // P chunk k (keys 32 c + 16 s2 + 4 half + {0..3, 8..11}, 2 e and 2 e + 1 of them): exp2, bf16, row sum
       auto softmax_chunk = [&](const f32x16 (&sc)[2], int k) {
         const int c = k / 8, s2 = (k / 4) % 2, e = k % 4;
-        const float p0 = fast_exp2(sc[c][8 * s2 + 2 * e] - m);
-        const float p1 = fast_exp2(sc[c][8 * s2 + 2 * e + 1] - m);
+        const float p0 = fast_exp2(sc[c][8 * s2 + 2 * e]);
+        const float p1 = fast_exp2(sc[c][8 * s2 + 2 * e + 1]);
         pb[c][s2][e] = pack_bf2(p0, p1);
         psum = dot2_bf16_sum(pb[c][s2][e], psum);
       };
-      sn[0] = f32x16{};
-      sn[1] = f32x16{};
+      {
+        f32x16 nm;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) nm[r] = -m;
+        sn[0] = nm;   // the QK MFMAs accumulate onto -m: S - m with no subtraction per score
+        sn[1] = nm;
+      }
 #pragma unroll
       for (int j = 0; j < PF; ++j) kr[j] = kread(j);
 #pragma unroll
@@ -418,14 +427,18 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
       }
       l += psum;
       mx = xhalf_max(mx);
-      if (__any(mx > m + RESCALE_T)) {
+      if (__any(mx > RESCALE_T)) {
         asm volatile("" ::: "memory");   // a branch, not 4 DT + 1 speculated multiplies per tile
-        const float mnew = fmaxf(m, mx);
-        const float alpha = fast_exp2(m - mnew);
+        const float d = fmaxf(mx, 0.f);   // new m - m
+        const float alpha = fast_exp2(-d);
         l *= alpha;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
-        m = mnew;
+        m += d;
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) sn[c][r] -= d;
       }
       if (t & 1) __syncthreads();
     };
