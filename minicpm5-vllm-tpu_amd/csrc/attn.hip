@@ -415,7 +415,7 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
           constexpr int NM = NPV - NPC;
 #pragma unroll
           for (int k = (j - NPC) * NCH / NM; k < (j - NPC + 1) * NCH / NM; ++k)
-            mx = fmaxf(mx, fmaxf(sn[k / 8][2 * (k % 8)], sn[k / 8][2 * (k % 8) + 1]));
+            mx = fmaxf(fmaxf(mx, sn[k / 8][2 * (k % 8)]), sn[k / 8][2 * (k % 8) + 1]);
         }
         if (j == NPV / 2) {
           // K(t+3) and V(t+2) into the slots K(t-1) and V(t-2) left (last read in steps t-2): their
