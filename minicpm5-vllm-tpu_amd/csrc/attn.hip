@@ -11,7 +11,8 @@
 //   * attn_fwd_kernel: one workgroup = (sequence, kv head, two 32-token q tiles paired
 //     zig-zag so every workgroup does the same causal work).  Its 8 waves are the 8 q heads of the
 //     kv head (GQA stacking, mk_attn.py:584-589); they share every K / V^T tile staged in LDS
-//     (double-buffered, prefetched through registers).  Each wave computes S^T = K Q^T with
+//     (4-slot rings filled through registers, a barrier every second key tile).  Each wave computes
+//     S^T = K Q^T, accumulated onto -m so the scores arrive relative to the running max, with
 //     v_mfma_f32_32x32x16_bf16, so a lane owns one query's scores (column of the tile) and the
 //     row max / row sum need only in-lane work plus one exchange between the two lane halves.
 //     The accumulator layout of S^T is exactly the B-operand layout P^T needs for O^T = V^T P^T,
