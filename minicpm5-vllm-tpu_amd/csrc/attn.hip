@@ -11,7 +11,7 @@
 //   * attn_fwd_kernel: one workgroup = (sequence, kv head, two 32-token q tiles paired
 //     zig-zag so every workgroup does the same causal work).  Its 8 waves are the 8 q heads of the
 //     kv head (GQA stacking, mk_attn.py:584-589); they share every K / V^T tile staged in LDS
-//     (4-slot rings filled through registers, a barrier every second key tile).  Each wave computes
+//     (4-slot rings filled by direct global -> LDS copies, a barrier every second key tile).  Each wave computes
 //     S^T = K Q^T, accumulated onto -m so the scores arrive relative to the running max, with
 //     v_mfma_f32_32x32x16_bf16, so a lane owns one query's scores (column of the tile) and the
 //     row max / row sum need only in-lane work plus one exchange between the two lane halves.
@@ -78,10 +78,17 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(const uint16_t* __restri
     }
   }
   __syncthreads();
+  // V^T is written with bits 2 and 3 of the key index swapped inside each 16-key group: 16-byte
+  // chunk 2 g + h of a row holds keys 16 g + 4 h + {0..3} and 16 g + 8 + 4 h + {0..3}, the 8 keys one
+  // lane's P^T column covers in the attention kernel, so that kernel copies V^T tiles into LDS as
+  // plain 16-byte chunks
   uint16_t* vdst = vt + ((size_t)b * n_kv + kv) * HD * S + t0;
   for (int idx = tid; idx < HD * 8; idx += 256) {
     const int d = idx / 8, c = idx % 8;
-    *reinterpret_cast<u32x4*>(vdst + (size_t)d * S + 8 * c) = *reinterpret_cast<const u32x4*>(&vs[d][8 * c]);
+    const int k0 = 16 * (c >> 1) + 4 * (c & 1);
+    const u32x2 lo = *reinterpret_cast<const u32x2*>(&vs[d][k0]);
+    const u32x2 hi = *reinterpret_cast<const u32x2*>(&vs[d][k0 + 8]);
+    *reinterpret_cast<u32x4*>(vdst + (size_t)d * S + 8 * c) = u32x4{lo[0], lo[1], hi[0], hi[1]};
   }
 }
 
@@ -96,10 +103,6 @@ struct AttnSmem {
   // barrier is needed only every second step
   static constexpr int NK = 4, NV = 4;
   static constexpr int TOTAL = NK * KBYTES + NV * VBYTES;
-  static constexpr int KCH = KT * HD / 8;    // 16-byte chunks per K tile
-  static constexpr int VCH = HD * KT / 8;    // 16-byte chunks per V^T tile
-  static constexpr int KPT = (KCH + NT - 1) / NT;
-  static constexpr int VPT = (VCH + NT - 1) / NT;
   static_assert(G * QT * (HD * 2 + 16) <= TOTAL, "output staging must fit in the K/V rings");
 };
 
@@ -159,50 +162,47 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
   const uint16_t* kg = krope + ((size_t)b * n_kv + kv) * (size_t)S * HD;
   const uint16_t* vg = vt + ((size_t)b * n_kv + kv) * (size_t)HD * S;
 
-  u32x4 kst[L::KPT], vst[L::VPT];
-  auto gload_k = [&](int kt, u32x4 (&kst)[L::KPT]) {
+  // K / V^T tiles reach LDS by direct global -> LDS copies (global_load_lds_dwordx4, no VGPR staging).
+  // The LDS image of a tile is its padded rows (K: KROW bytes = HD / 8 + 1 chunks per key; V^T: VROW
+  // bytes = 9 chunks per d row) as consecutive 16-byte chunks, and one wave instruction fills 64 of
+  // them: lane l of instruction i fills image chunk 64 i + l.  A lane that lands on a pad chunk copies
+  // a valid chunk of its row (pads are never read).  V^T comes from the prep kernel with its keys
+  // already in the order the PV operand reads need.
+  constexpr int KRC = L::KROW / 16, VRC = L::VROW / 16;
+  constexpr int KIN = KT * KRC / 64;                 // instructions per K tile (64 rows: exact)
+  constexpr int VIN = (HD * VRC + 63) / 64;          // per V^T tile (the last one partial at hd 96)
+  constexpr int KIW = (KIN + G - 1) / G, VIW = (VIN + G - 1) / G;   // per wave, at most
+  static_assert(KT * KRC % 64 == 0, "K image is whole instructions");
+  uint32_t koff[KIW], voff[VIW];                     // element offset of this lane's chunk in a tile
 #pragma unroll
-    for (int i = 0; i < L::KPT; ++i) {
-      const int c = tid + i * NT;
-      if (L::KCH % NT == 0 || c < L::KCH) {
-        const int key = c / (HD / 8), dc = c % (HD / 8);
-        kst[i] = *reinterpret_cast<const u32x4*>(kg + (size_t)(kt * KT + key) * HD + dc * 8);
-      }
+  for (int i = 0; i < KIW; ++i) {
+    const int ch = 64 * (w + G * i) + lane;
+    const int row = min(ch / KRC, KT - 1), pos = ch % KRC;
+    koff[i] = row * HD + (pos < HD / 8 ? pos : 0) * 8;
+  }
+#pragma unroll
+  for (int i = 0; i < VIW; ++i) {
+    const int ch = 64 * (w + G * i) + lane;
+    const int d = min(ch / VRC, HD - 1), pos = ch % VRC;
+    voff[i] = d * S + (pos < KT / 8 ? pos : 0) * 8;
+  }
+  auto aload_k = [&](int kt, int slot) {
+    const uint16_t* src = kg + (size_t)kt * KT * HD;
+    char* dst = kring + slot * L::KBYTES;
+#pragma unroll
+    for (int i = 0; i < KIW; ++i) {
+      const int ins = w + G * i;
+      if (KIN % G == 0 || ins < KIN) copy16_to_lds(src + koff[i], dst + 1024 * ins);
     }
   };
-  auto gload_v = [&](int kt, u32x4 (&vst)[L::VPT]) {
+  auto aload_v = [&](int kt, int slot) {
+    const uint16_t* src = vg + (size_t)kt * KT;
+    char* dst = vring + slot * L::VBYTES;
 #pragma unroll
-    for (int i = 0; i < L::VPT; ++i) {
-      const int c = tid + i * NT;
-      if (L::VCH % NT == 0 || c < L::VCH) {
-        const int d = c / (KT / 8), kc = c % (KT / 8);
-        vst[i] = *reinterpret_cast<const u32x4*>(vg + (size_t)d * S + kt * KT + kc * 8);
-      }
-    }
-  };
-  auto sstore_k = [&](int slot, const u32x4 (&kst)[L::KPT]) {
-    char* ks = kring + slot * L::KBYTES;
-#pragma unroll
-    for (int i = 0; i < L::KPT; ++i) {
-      const int c = tid + i * NT;
-      if (L::KCH % NT == 0 || c < L::KCH) {
-        const int key = c / (HD / 8), dc = c % (HD / 8);
-        *reinterpret_cast<u32x4*>(ks + key * L::KROW + dc * 16) = kst[i];
-      }
-    }
-  };
-  auto sstore_v = [&](int slot, const u32x4 (&vst)[L::VPT]) {
-    char* vs = vring + slot * L::VBYTES;
-#pragma unroll
-    for (int i = 0; i < L::VPT; ++i) {
-      const int c = tid + i * NT;
-      if (L::VCH % NT == 0 || c < L::VCH) {
-        // keys are stored with bits 2 and 3 of their index swapped inside each 16-key group, so the 8
-        // keys a lane's P^T column holds (4 half + {0..3, 8..11}) are 16 contiguous bytes
-        const int d = c / (KT / 8), kc = c % (KT / 8);
-        char* row = vs + d * L::VROW + (kc >> 1) * 32 + (kc & 1) * 8;
-        *reinterpret_cast<u32x2*>(row) = u32x2{vst[i][0], vst[i][1]};        // keys 8 kc + 0..3
-        *reinterpret_cast<u32x2*>(row + 16) = u32x2{vst[i][2], vst[i][3]};   // keys 8 kc + 4..7
+    for (int i = 0; i < VIW; ++i) {
+      const int ins = w + G * i;
+      if (VIN % G == 0 || ins < VIN) {
+        if (HD * VRC % 64 == 0 || 64 * ins + lane < HD * VRC) copy16_to_lds(src + voff[i], dst + 1024 * ins);
       }
     }
   };
@@ -314,19 +314,12 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
 
     // ---- prologue: K(0..2), V(0..1) staged (indices clamped to the last tile); S(0) computed
     __syncthreads();   // the previous pass (output staging) is done with the LDS
-    {
-      u32x4 k1[L::KPT], k2[L::KPT], v1[L::VPT];
-      gload_k(0, kst);
-      gload_v(0, vst);
-      gload_k(min(1, nkt - 1), k1);
-      gload_v(min(1, nkt - 1), v1);
-      gload_k(min(2, nkt - 1), k2);
-      sstore_k(0, kst);
-      sstore_v(0, vst);
-      sstore_k(1, k1);
-      sstore_v(1, v1);
-      sstore_k(2, k2);
-    }
+    aload_k(0, 0);
+    aload_v(0, 0);
+    aload_k(min(1, nkt - 1), 1);
+    aload_v(min(1, nkt - 1), 1);
+    aload_k(min(2, nkt - 1), 2);
+    __builtin_amdgcn_s_waitcnt(0);   // this wave's copies have landed
     __syncthreads();
     f32x16 scur[2], snext[2];
     qk(0, scur);
@@ -351,8 +344,10 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
     static_assert(NPC < NPV && softmax_deadlines_ok(NQC, DT), "softmax chunks must be ready for their PV MFMAs");
     auto step = [&](auto mask, int t, const f32x16 (&sc)[2], f32x16 (&sn)[2]) {
       constexpr bool MASK = decltype(mask)::value;
-      gload_k(min(t + 3, nkt - 1), kst);   // clamped reloads at the end land in free slots
-      gload_v(min(t + 2, nkt - 1), vst);
+      // K(t+3), V(t+2) into the slots K(t-1), V(t-2) left (last read in step t-2); clamped reloads at
+      // the end land in free slots.  The copies are awaited before the next barrier.
+      aload_k(min(t + 3, nkt - 1), (t + 3) % L::NK);
+      aload_v(min(t + 2, nkt - 1), (t + 2) % L::NV);
       const char* ksl = kring + ((t + 1) % L::NK) * L::KBYTES;
       auto kread = [&](int j) {
         const int s = j / 2, c = j % 2;
@@ -418,12 +413,6 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
           for (int k = (j - NPC) * NCH / NM; k < (j - NPC + 1) * NCH / NM; ++k)
             mx = fmaxf(fmaxf(mx, sn[k / 8][2 * (k % 8)]), sn[k / 8][2 * (k % 8) + 1]);
         }
-        if (j == NPV / 2) {
-          // K(t+3) and V(t+2) into the slots K(t-1) and V(t-2) left (last read in steps t-2): their
-          // global loads were issued at the start of the step
-          sstore_k((t + 3) % L::NK, kst);
-          sstore_v((t + 2) % L::NV, vst);
-        }
         __builtin_amdgcn_sched_barrier(0);
       }
       l += psum;
@@ -441,7 +430,10 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
 #pragma unroll
           for (int r = 0; r < 16; ++r) sn[c][r] -= d;
       }
-      if (t & 1) __syncthreads();
+      if (t & 1) {
+        __builtin_amdgcn_s_waitcnt(0);   // this wave's copies of steps t-1 and t have landed
+        __syncthreads();
+      }
     };
     using Plain = std::integral_constant<bool, false>;
     using Diag = std::integral_constant<bool, true>;
@@ -462,6 +454,7 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
       scur[1] = snext[1];
     }
     softmax_pv((nkt - 1) % L::NV, scur);
+    __builtin_amdgcn_s_waitcnt(0);   // no copy still in flight into the rings
     __syncthreads();   // every wave is done with the rings before the output staging reuses them
 
     l = xhalf_sum(l);

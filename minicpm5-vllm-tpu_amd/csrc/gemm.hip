@@ -136,15 +136,6 @@ __device__ inline void epi_store(const GemmArgs& g, int m, int n, float v) {
 // rows, same chunk) hit 16 distinct 4-bank groups.
 __device__ inline int swz(int row) { return (row >> 2) & 3; }
 
-typedef __attribute__((address_space(3))) void* lds_ptr;
-
-// 16-byte global -> LDS copy that bypasses VGPRs (global_load_lds_dwordx4).  Kept in a non-template
-// function: in a template kernel with dependent arguments the host pass of clang rejects the builtin
-// silently and then emits no launch stub for the kernel.
-__device__ inline void copy16_to_lds(const char* src, char* dst) {
-  __builtin_amdgcn_global_load_lds(src, (lds_ptr)dst, 16, 0, 0);
-}
-
 // Workgroup barrier for the LDS ring.  A bare s_barrier: __syncthreads() adds a fence that would also
 // drain the younger stages' async loads.  The empty asm statements keep the compiler from moving LDS
 // accesses across it.

@@ -88,6 +88,16 @@ __device__ inline uint32_t pack_fp8x4(float a, float b, float c, float d) {
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+typedef __attribute__((address_space(3))) void* lds_ptr;
+
+// 16-byte global -> LDS copy that bypasses VGPRs (global_load_lds_dwordx4): lane l of the wave writes
+// dst + 16 l, so dst must be the same for every lane.  Completion is counted by vmcnt.  Kept in a
+// non-template function: in a template kernel with dependent arguments the host pass of clang rejects
+// the builtin silently and then emits no launch stub for the kernel.
+__device__ inline void copy16_to_lds(const void* src, char* dst) {
+  __builtin_amdgcn_global_load_lds(src, (lds_ptr)dst, 16, 0, 0);
+}
+
 // acc + lo(w) + hi(w) for a packed bf16 pair (v_dot2_f32_bf16 with (1, 1))
 __device__ inline float dot2_bf16_sum(uint32_t w, float acc) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), __builtin_bit_cast(bf16x2, 0x3f803f80u),
