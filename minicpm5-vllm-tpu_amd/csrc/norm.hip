@@ -122,13 +122,16 @@ __global__ __launch_bounds__(256) void rowquant_kernel(QuantArgs a) {
       w0 = pack_fp8x4(t[0], t[1], t[2], t[3]);
       w1 = pack_fp8x4(t[4], t[5], t[6], t[7]);
     } else {
+      // q = clip(round_half_even(t), -127, 127), clipped first (the same for a monotonic rounding):
+      // adding 1.5 * 2^23 rounds the clipped value to an integer in the default round-to-nearest-even
+      // mode and leaves it, two's complement, in the low byte of the sum's bit pattern
+      uint32_t qb[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float q = fminf(fmaxf(rintf(t[e]), -127.f), 127.f);
-        const uint32_t b = static_cast<uint32_t>(static_cast<int32_t>(q)) & 0xffu;
-        if (e < 4) w0 |= b << (8 * e);
-        else w1 |= b << (8 * (e - 4));
-      }
+      for (int e = 0; e < 8; ++e) qb[e] = __float_as_uint(__fadd_rn(fminf(fmaxf(t[e], -127.f), 127.f), 12582912.f));
+      // bytes 0 of four words -> one word (v_perm_b32 selector bytes: 0..3 from the second source,
+      // 4..7 from the first, 0x0c = zero)
+      w0 = __builtin_amdgcn_perm(qb[1], qb[0], 0x0c0c0400u) | __builtin_amdgcn_perm(qb[3], qb[2], 0x04000c0cu);
+      w1 = __builtin_amdgcn_perm(qb[5], qb[4], 0x0c0c0400u) | __builtin_amdgcn_perm(qb[7], qb[6], 0x04000c0cu);
     }
     *reinterpret_cast<u32x2*>(qrow + 8 * c) = u32x2{w0, w1};
   }
