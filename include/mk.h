@@ -144,7 +144,8 @@ int mk_forward_timed(mk_model* m, const int32_t* input_ids, int bs, int seq, voi
 /* Causal GQA prefill attention (super_gqa_v2, mk_attn.py:660-710): qkv (B, S, (n_q + 2 n_kv) hd) bf16
  * -> out (B, S, n_q hd) bf16, RoPE from the bf16 cos / sin tables applied in-kernel, softmax in f32
  * with scores scaled by sm_scale (pass 1.0 when 1/sqrt(hd) is folded into W_q, as the plugin does).
- * scratch: mk_attn_scratch_bytes(B, S, n_kv, hd) bytes. */
+ * scratch: mk_attn_scratch_bytes(B, S, n_kv, hd) bytes (RoPE'd K, V transposed, and one work-queue counter per
+ * kv head, so n_kv <= 63); calls that share one scratch buffer must not overlap. */
 size_t mk_attn_scratch_bytes(int B, int S, int n_kv, int head_dim);
 int mk_attn_prefill(const void* qkv, const void* cos, const void* sin, void* out, void* scratch,
                     size_t scratch_bytes, int B, int S, int n_q, int n_kv, int head_dim, float sm_scale,

@@ -37,7 +37,9 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(const uint16_t* __restri
                                                         const uint16_t* __restrict__ sinr,
                                                         uint16_t* __restrict__ krope,
                                                         uint16_t* __restrict__ vt, int S, int n_q,
-                                                        int n_kv) {
+                                                        int n_kv, int* __restrict__ queue) {
+  // the attention kernel's work queues start empty (vector atomics: no scalar-cache writes)
+  if (blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && threadIdx.x <= n_kv) atomicExch(&queue[threadIdx.x], 0);
   // 64 tokens of one kv head; 16-byte loads and stores throughout.  V goes through LDS for the
   // transpose (row of 64 tokens + 8 pad elements: the column reads of 8 consecutive tokens spread
   // over the banks).
@@ -136,31 +138,36 @@ template <int HD>
 __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
     const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ cosr,
     const uint16_t* __restrict__ sinr, const uint16_t* __restrict__ krope,
-    const uint16_t* __restrict__ vt, uint16_t* __restrict__ out, int S, int n_q, int n_kv,
-    float qscale) {
+    const uint16_t* __restrict__ vt, uint16_t* __restrict__ out, int B, int S, int n_q, int n_kv,
+    float qscale, int* __restrict__ queue) {
   using L = AttnSmem<HD>;
   constexpr int KS = HD / 16;   // k-steps of QK^T
   constexpr int DT = HD / 32;   // 32-row d tiles of O^T
-  __shared__ __attribute__((aligned(16))) char smem[L::TOTAL];
+  // the rings, then the work item handed from thread 0 to the workgroup (one LDS object: a second
+  // one makes the compiler wait for the in-flight ring copies before every LDS read)
+  __shared__ __attribute__((aligned(16))) char smem[L::TOTAL + 16];
+  int* const item_s = reinterpret_cast<int*>(smem + L::TOTAL);
   char* const kring = smem;
   char* const vring = smem + L::NK * L::KBYTES;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
   const int col = lane & 31, half = lane >> 5;
-  // XCD-aware work mapping: workgroups are dispatched round-robin over the 8 XCDs (each with its
-  // own L2); consecutive logical work items (same sequence and kv head) go to the same XCD so its
-  // L2 serves one kv head's K / V^T stream.
-  const int nblk = gridDim.x * gridDim.y * gridDim.z;
-  const int lid = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
-  const int work = (nblk % 8 == 0) ? (lid % 8) * (nblk / 8) + lid / 8 : lid;
-  const int pair = work % gridDim.x;
-  const int kv = (work / gridDim.x) % n_kv, b = work / (gridDim.x * n_kv);
+  // Work items are (kv head, sequence, 32-token q tile), taken from one queue per kv head (an atomic
+  // counter), longest tiles first.  The grid is one persistent workgroup per CU: a workgroup takes
+  // items from the queue of its XCD's kv head (XCD id mod n_kv, so an XCD's L2 serves one kv head's
+  // K / V^T stream) and, when that queue is empty, from the others.  The XCDs run at different clocks
+  // (up to 6 % apart); a static split would end with the slowest one.  Which workgroup computes an
+  // item does not change its result.
   const int ntiles = S / QT;
+  const int nper = B * ntiles;                       // items per kv head
   const int D = (n_q + 2 * n_kv) * HD;
-  const int head = kv * G + w;
-  const uint16_t* kg = krope + ((size_t)b * n_kv + kv) * (size_t)S * HD;
-  const uint16_t* vg = vt + ((size_t)b * n_kv + kv) * (size_t)HD * S;
+  unsigned xcc;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+  const int xq = (int)(xcc & 15u) % n_kv;
+  int head = 0;
+  const uint16_t* kg = krope;
+  const uint16_t* vg = vt;
 
   // K / V^T tiles reach LDS by direct global -> LDS copies (global_load_lds_dwordx4, no VGPR staging).
   // The LDS image of a tile is its padded rows (K: KROW bytes = HD / 8 + 1 chunks per key; V^T: VROW
@@ -207,8 +214,26 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
     }
   };
 
-  for (int pass = 0; pass < 2; ++pass) {
-    const int qt = pass == 0 ? pair : ntiles - 1 - pair;
+  for (;;) {
+    if (tid == 0) {
+      int it = -1;
+      for (int k = 0; k < n_kv; ++k) {
+        const int q = (xq + k) % n_kv;
+        const int v = atomicAdd(&queue[q], 1);
+        if (v >= 0 && v < nper) {
+          it = q * nper + v;
+          break;
+        }
+      }
+      *item_s = it;
+    }
+    __syncthreads();
+    const int item = *item_s;
+    if (item < 0) break;
+    const int kv = item / nper, qt = ntiles - 1 - (item % nper) / B, b = (item % nper) % B;
+    head = kv * G + w;
+    kg = krope + ((size_t)b * n_kv + kv) * (size_t)S * HD;
+    vg = vt + ((size_t)b * n_kv + kv) * (size_t)HD * S;
     const int t0 = qt * QT;
     const int tok = t0 + col;
 
@@ -484,20 +509,44 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
       }
     }
   }
+  // the last workgroup out resets the queues for the next launch; the fence orders this workgroup's
+  // queue atomics before its count
+  if (tid == 0) {
+    __threadfence();
+    const int done = atomicAdd(&queue[n_kv], 1);
+    if (done == (int)(gridDim.x * gridDim.y * gridDim.z) - 1) {
+      __threadfence();
+      for (int q = 0; q <= n_kv; ++q) atomicExch(&queue[q], 0);
+    }
+  }
+}
+
+// work-queue counters (n_kv item counters + a done counter) after K and V^T in the scratch
+inline int* attn_queue(const AttnArgs& a) {
+  return reinterpret_cast<int*>(a.vt + (size_t)a.B * a.n_kv * a.hd * a.S);
 }
 
 template <int HD>
 int launch_attn_hd(const AttnArgs& a, hipStream_t st, int stages) {
+  int* queue = attn_queue(a);
   if (stages & 1) {
     const dim3 pg(a.S / 64, a.n_kv, a.B);
     hipLaunchKernelGGL(attn_prep_kernel<HD>, pg, dim3(256), 0, st, a.qkv, a.cos, a.sin, a.krope, a.vt,
-                       a.S, a.n_q, a.n_kv);
+                       a.S, a.n_q, a.n_kv, queue);
     MK_HIP_CHECK(hipGetLastError());
   }
   if (stages & 2) {
-    const dim3 fg(a.S / QT / 2, a.n_kv, a.B);
+    // one persistent workgroup per CU (a workgroup's LDS fills a CU), at most one per work item
+    static const int ncu = [] {
+      int dev = 0, n = 0;
+      if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        n = 0;
+      return n > 0 ? n : 256;
+    }();
+    const int items = a.B * a.n_kv * (a.S / QT);
+    const dim3 fg(items < ncu ? items : ncu);
     hipLaunchKernelGGL(attn_fwd_kernel<HD>, fg, dim3(NT), 0, st, a.qkv, a.cos, a.sin, a.krope, a.vt,
-                       a.out, a.S, a.n_q, a.n_kv, a.qscale);
+                       a.out, a.B, a.S, a.n_q, a.n_kv, a.qscale, queue);
     MK_HIP_CHECK(hipGetLastError());
   }
   return MK_OK;
@@ -667,13 +716,14 @@ int attn_validate(int B, int S, int n_q, int n_kv, int hd) {
   MK_REQUIRE(B >= 1, "attention: batch must be >= 1");
   MK_REQUIRE(S >= 64 && S % 64 == 0, "attention: seq must be a positive multiple of 64");
   MK_REQUIRE(n_kv >= 1 && n_q == G * n_kv, "attention: n_q must equal 8 * n_kv (GQA group of 8)");
+  MK_REQUIRE(n_kv <= 63, "attention: at most 63 kv heads (one work-queue counter each)");
   MK_REQUIRE(hd == 64 || hd == 96 || hd == 128, "attention: head_dim must be 64, 96 or 128");
   return MK_OK;
 }
 
 size_t attn_scratch_bytes(int B, int S, int n_kv, int hd) {
-  // RoPE'd K + transposed V, bf16.
-  return (size_t)2 * B * n_kv * S * hd * sizeof(uint16_t);
+  // RoPE'd K + transposed V, bf16, then the attention kernel's work-queue counters
+  return (size_t)2 * B * n_kv * S * hd * sizeof(uint16_t) + 256;
 }
 
 int launch_attn_stages(const AttnArgs& a, hipStream_t st, int stages) {

@@ -13,7 +13,7 @@ struct AttnArgs {
   const uint16_t* cos;   // (>= S, hd) bf16 RoPE table
   const uint16_t* sin;   // (>= S, hd) bf16
   uint16_t* krope;       // scratch (B, n_kv, S, hd) bf16: RoPE'd K
-  uint16_t* vt;          // scratch (B, n_kv, hd, S) bf16: V transposed
+  uint16_t* vt;          // scratch (B, n_kv, hd, S) bf16: V transposed, then the work-queue counters
   uint16_t* out;         // (B, S, n_q hd) bf16
   int B, S, n_q, n_kv, hd;
   float qscale;          // multiplies RoPE'd q before the bf16 rounding (sm_scale * log2 e)
@@ -21,7 +21,8 @@ struct AttnArgs {
 int attn_validate(int B, int S, int n_q, int n_kv, int hd);
 size_t attn_scratch_bytes(int B, int S, int n_kv, int hd);
 int launch_attn(const AttnArgs& a, hipStream_t st);
-// stages: 1 = K-RoPE / V-transpose prep, 2 = the attention kernel, 3 = both
+// stages: 1 = K-RoPE / V-transpose prep (also empties the work queues), 2 = the attention kernel
+// (leaves the queues empty for the next launch), 3 = both
 int launch_attn_stages(const AttnArgs& a, hipStream_t st, int stages);
 
 // Last-token attention of the last layer (mk_jax.py:492-520): one query per sequence over all S keys.

@@ -121,3 +121,21 @@ def test_ops_refuse_cpu_tensors():
     with pytest.raises(ops.MkError, match="GPU tensor"):
         ops.attn_prefill(torch.zeros(1, 256, 20 * 64, dtype=torch.bfloat16), torch.zeros(256, 64, dtype=torch.bfloat16),
                          torch.zeros(256, 64, dtype=torch.bfloat16), 16, 2, 64)
+
+
+@pytest.mark.parametrize("B,S,n_q,n_kv,hd,msg", [
+    (1, 8192, 512, 64, 128, "63 kv heads"),
+    (1, 8192, 16, 3, 128, "8 * n_kv"),
+    (1, 100, 16, 2, 128, "multiple of 64"),
+    (1, 8192, 16, 2, 80, "head_dim"),
+    (0, 8192, 16, 2, 128, "batch"),
+    (1, 8192, 16, 2, 128, "null pointer"),
+])
+def test_attn_prefill_rejects_before_launch(B, S, n_q, n_kv, hd, msg):
+    """mk_attn_prefill checks its shapes and pointers on the host and returns an error, no kernel launched."""
+    from minicpm5_mk import _lib
+
+    lib = _lib.load()
+    rc = lib.mk_attn_prefill(None, None, None, None, None, 0, B, S, n_q, n_kv, hd, 1.0, None)
+    assert rc != 0
+    assert msg in lib.mk_last_error().decode()
