@@ -134,7 +134,7 @@ __device__ inline float xhalf_sum(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-template <int HD>
+template <int HD, bool DYN>
 __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
     const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ cosr,
     const uint16_t* __restrict__ sinr, const uint16_t* __restrict__ krope,
@@ -153,18 +153,32 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
   const int col = lane & 31, half = lane >> 5;
-  // Work items are (kv head, sequence, 32-token q tile), taken from one queue per kv head (an atomic
-  // counter), longest tiles first.  The grid is one persistent workgroup per CU: a workgroup takes
-  // items from the queue of its XCD's kv head (XCD id mod n_kv, so an XCD's L2 serves one kv head's
-  // K / V^T stream) and, when that queue is empty, from the others.  The XCDs run at different clocks
-  // (up to 6 % apart); a static split would end with the slowest one.  Which workgroup computes an
-  // item does not change its result.
+  // Work items are (kv head, sequence, 32-token q tile).  Which workgroup computes an item does not
+  // change its result.
+  //  * static (!DYN): workgroup = (sequence, kv head, q tiles p and S/32-1-p), so every workgroup does
+  //    the same causal work; workgroups are dispatched round-robin over the 8 XCDs (each with its own
+  //    L2), and consecutive logical work (same sequence and kv head) is put on one XCD so its L2
+  //    serves one kv head's K / V^T stream.  Used when the pairs fill the CUs in whole rounds.
+  //  * DYN: one persistent workgroup per CU takes items from one queue per kv head (an atomic
+  //    counter), longest tiles first: from the queue of its XCD's kv head (XCD id mod n_kv) and, when
+  //    that one is empty, from the others.  Used for short or odd-sized launches.
   const int ntiles = S / QT;
   const int nper = B * ntiles;                       // items per kv head
   const int D = (n_q + 2 * n_kv) * HD;
-  unsigned xcc;
-  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
-  const int xq = (int)(xcc & 15u) % n_kv;
+  int xq = 0, pair = 0, skv = 0, sb = 0;
+  if constexpr (DYN) {
+    unsigned xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    xq = (int)(xcc & 15u) % n_kv;
+  } else {
+    const int nblk = gridDim.x * gridDim.y * gridDim.z;
+    const int lid = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+    const int work = (nblk % 8 == 0) ? (lid % 8) * (nblk / 8) + lid / 8 : lid;
+    const int npair = ntiles / 2;
+    pair = work % npair;
+    skv = (work / npair) % n_kv;
+    sb = work / (npair * n_kv);
+  }
   int head = 0;
   const uint16_t* kg = krope;
   const uint16_t* vg = vt;
@@ -214,23 +228,33 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
     }
   };
 
-  for (;;) {
-    if (tid == 0) {
-      int it = -1;
-      for (int k = 0; k < n_kv; ++k) {
-        const int q = (xq + k) % n_kv;
-        const int v = atomicAdd(&queue[q], 1);
-        if (v >= 0 && v < nper) {
-          it = q * nper + v;
-          break;
+  for (int pass = 0;; ++pass) {
+    int kv, qt, b;
+    if constexpr (DYN) {
+      if (tid == 0) {
+        int it = -1;
+        for (int k = 0; k < n_kv; ++k) {
+          const int q = (xq + k) % n_kv;
+          const int v = atomicAdd(&queue[q], 1);
+          if (v >= 0 && v < nper) {
+            it = q * nper + v;
+            break;
+          }
         }
+        *item_s = it;
       }
-      *item_s = it;
+      __syncthreads();
+      const int item = *item_s;
+      if (item < 0) break;
+      kv = item / nper;
+      qt = ntiles - 1 - (item % nper) / B;
+      b = (item % nper) % B;
+    } else {
+      if (pass == 2) break;
+      kv = skv;
+      b = sb;
+      qt = pass == 0 ? pair : ntiles - 1 - pair;
     }
-    __syncthreads();
-    const int item = *item_s;
-    if (item < 0) break;
-    const int kv = item / nper, qt = ntiles - 1 - (item % nper) / B, b = (item % nper) % B;
     head = kv * G + w;
     kg = krope + ((size_t)b * n_kv + kv) * (size_t)S * HD;
     vg = vt + ((size_t)b * n_kv + kv) * (size_t)HD * S;
@@ -511,7 +535,7 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
   }
   // the last workgroup out resets the queues for the next launch; the fence orders this workgroup's
   // queue atomics before its count
-  if (tid == 0) {
+  if (DYN && tid == 0) {
     __threadfence();
     const int done = atomicAdd(&queue[n_kv], 1);
     if (done == (int)(gridDim.x * gridDim.y * gridDim.z) - 1) {
@@ -543,10 +567,16 @@ int launch_attn_hd(const AttnArgs& a, hipStream_t st, int stages) {
         n = 0;
       return n > 0 ? n : 256;
     }();
-    const int items = a.B * a.n_kv * (a.S / QT);
-    const dim3 fg(items < ncu ? items : ncu);
-    hipLaunchKernelGGL(attn_fwd_kernel<HD>, fg, dim3(NT), 0, st, a.qkv, a.cos, a.sin, a.krope, a.vt,
-                       a.out, a.B, a.S, a.n_q, a.n_kv, a.qscale, queue);
+    // static pairs when they fill the CUs in whole rounds (no queue atomics, fixed XCD placement),
+    // else the work queues
+    const int items = a.B * a.n_kv * (a.S / QT), pairs = items / 2;
+    if (pairs % ncu == 0) {
+      hipLaunchKernelGGL((attn_fwd_kernel<HD, false>), dim3(pairs), dim3(NT), 0, st, a.qkv, a.cos, a.sin,
+                         a.krope, a.vt, a.out, a.B, a.S, a.n_q, a.n_kv, a.qscale, queue);
+    } else {
+      hipLaunchKernelGGL((attn_fwd_kernel<HD, true>), dim3(items < ncu ? items : ncu), dim3(NT), 0, st, a.qkv,
+                         a.cos, a.sin, a.krope, a.vt, a.out, a.B, a.S, a.n_q, a.n_kv, a.qscale, queue);
+    }
     MK_HIP_CHECK(hipGetLastError());
   }
   return MK_OK;

@@ -75,6 +75,24 @@ def test_attention_deterministic():
     assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("B,S,hd", [(2, 4096, 128), (4, 2048, 96)])
+def test_attention_batch_invariant(B, S, hd):
+    """Each sequence of a batch equals the same sequence run alone, bit for bit.  The batch launches
+    (B * 2 kv heads * S / 64 tile pairs = 256) take the static pair mapping, the single-sequence ones
+    the work queues, so this also checks that both mappings give identical results."""
+    from minicpm5_mk import ops
+    from minicpm5_mk.mk_weights import rope_tables
+
+    dev = _dev()
+    print(f"[attn-batch] B={B} S={S} hd={hd}", flush=True)
+    qkv = _attn_inputs(B, S, hd).to(dev)
+    cos, sin = (t.to(dev) for t in rope_tables(S, hd, 5e6))
+    full = ops.attn_prefill(qkv, cos, sin, 16, 2, hd)
+    for b in range(B):
+        one = ops.attn_prefill(qkv[b:b + 1].contiguous(), cos, sin, 16, 2, hd)
+        assert torch.equal(full[b:b + 1], one), b
+
+
 @pytest.mark.parametrize("T,H,norm,recip,f32", [(300, 1536, True, True, False), (64, 2048, False, False, False),
                                                 (129, 4608, False, True, True), (8192, 1536, True, True, False)])
 def test_row_quant_bitexact(T, H, norm, recip, f32):
