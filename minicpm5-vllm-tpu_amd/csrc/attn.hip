@@ -180,10 +180,9 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
     sb = work / (npair * n_kv);
   }
   int head = 0;
-  const uint16_t* kg = krope;
-  const uint16_t* vg = vt;
+  __amdgpu_buffer_rsrc_t krs, vrs;   // the item's K and V^T, as buffers for the ring copies
 
-  // K / V^T tiles reach LDS by direct global -> LDS copies (global_load_lds_dwordx4, no VGPR staging).
+  // K / V^T tiles reach LDS by direct memory -> LDS copies (buffer_load_dwordx4 ... lds, no VGPR staging).
   // The LDS image of a tile is its padded rows (K: KROW bytes = HD / 8 + 1 chunks per key; V^T: VROW
   // bytes = 9 chunks per d row) as consecutive 16-byte chunks, and one wave instruction fills 64 of
   // them: lane l of instruction i fills image chunk 64 i + l.  A lane that lands on a pad chunk copies
@@ -208,22 +207,21 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
     voff[i] = d * S + (pos < KT / 8 ? pos : 0) * 8;
   }
   auto aload_k = [&](int kt, int slot) {
-    const uint16_t* src = kg + (size_t)kt * KT * HD;
     char* dst = kring + slot * L::KBYTES;
 #pragma unroll
     for (int i = 0; i < KIW; ++i) {
       const int ins = w + G * i;
-      if (KIN % G == 0 || ins < KIN) copy16_to_lds(src + koff[i], dst + 1024 * ins);
+      if (KIN % G == 0 || ins < KIN) copy16_to_lds(krs, 2u * (kt * KT * HD + koff[i]), dst + 1024 * ins);
     }
   };
   auto aload_v = [&](int kt, int slot) {
-    const uint16_t* src = vg + (size_t)kt * KT;
     char* dst = vring + slot * L::VBYTES;
 #pragma unroll
     for (int i = 0; i < VIW; ++i) {
       const int ins = w + G * i;
       if (VIN % G == 0 || ins < VIN) {
-        if (HD * VRC % 64 == 0 || 64 * ins + lane < HD * VRC) copy16_to_lds(src + voff[i], dst + 1024 * ins);
+        if (HD * VRC % 64 == 0 || 64 * ins + lane < HD * VRC)
+          copy16_to_lds(vrs, 2u * (kt * KT + voff[i]), dst + 1024 * ins);
       }
     }
   };
@@ -256,8 +254,8 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
       qt = pass == 0 ? pair : ntiles - 1 - pair;
     }
     head = kv * G + w;
-    kg = krope + ((size_t)b * n_kv + kv) * (size_t)S * HD;
-    vg = vt + ((size_t)b * n_kv + kv) * (size_t)HD * S;
+    krs = make_rsrc(krope + ((size_t)b * n_kv + kv) * (size_t)S * HD, S * HD * 2);
+    vrs = make_rsrc(vt + ((size_t)b * n_kv + kv) * (size_t)HD * S, S * HD * 2);
     const int t0 = qt * QT;
     const int tok = t0 + col;
 

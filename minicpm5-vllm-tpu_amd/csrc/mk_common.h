@@ -98,6 +98,19 @@ __device__ inline void copy16_to_lds(const void* src, char* dst) {
   __builtin_amdgcn_global_load_lds(src, (lds_ptr)dst, 16, 0, 0);
 }
 
+// The same copy in buffer form (buffer_load_dwordx4 ... lds): dst + 16 l <- the 16 bytes at byte
+// offset `off` of the buffer `r` (offsets beyond its size read zeros).  Preferred in loops that read
+// LDS while copies are in flight: the compiler counts the global (FLAT-encoded) form as an access
+// that may go to LDS as well as memory, and while one is outstanding it makes every LDS read wait for
+// all earlier LDS reads (lgkmcnt(0)), which defeats operand prefetching; the buffer form is counted
+// by vmcnt alone.  Non-template for the same reason as copy16_to_lds.
+__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+__device__ inline void copy16_to_lds(__amdgpu_buffer_rsrc_t r, uint32_t off, char* dst) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)dst, 16, off, 0, 0, 0);
+}
+
 // acc + lo(w) + hi(w) for a packed bf16 pair (v_dot2_f32_bf16 with (1, 1))
 __device__ inline float dot2_bf16_sum(uint32_t w, float acc) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), __builtin_bit_cast(bf16x2, 0x3f803f80u),
