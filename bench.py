@@ -37,7 +37,7 @@ PEAK = {"bf16": 2516.6, "int8": 5033.2, "fp8": 5033.2, "hbm": 8000.0}   # MI355X
 METRIC = "prefill tokens/sec at (B,8192) B=1..32, 1B and 2B arch; p50 ms at (1,8192)"
 # HBM bytes per attn_fwd_kernel launch measured by rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (scaled by a
 # 256 MiB copy's counters) for the default workload; profiles/mfma_util_hbm_1b_b1_s8192.txt
-ATTN_TRAFFIC = {("1b", 1, 8192, "auto"): (91.3e6 + 43.0e6)}
+ATTN_TRAFFIC = {("1b", 1, 8192, "auto"): (77.1e6 + 33.6e6)}
 
 
 def log(*a):
