@@ -386,7 +386,7 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
     // MFMA is issued with a slice of the VALU work; LDS operands are read PF MFMAs ahead.  Only the last
     // key tile crosses the diagonal, so the causal mask lives in the MASK instance of the step alone.
     constexpr int NQK = 2 * KS, NPV = 4 * DT, NCH = 16, PF = 3;
-    constexpr int NQC = HD == 64 ? 12 : 8;   // softmax chunks computed in the QK loop
+    constexpr int NQC = HD == 128 ? 8 : 12;  // softmax chunks computed in the QK loop (measured best)
     constexpr int NPC = NCH - NQC;           // the rest: one per PV MFMA, then the row max
     static_assert(NPC < NPV && softmax_deadlines_ok(NQC, DT), "softmax chunks must be ready for their PV MFMAs");
     auto step = [&](auto mask, int t, const f32x16 (&sc)[2], f32x16 (&sn)[2]) {
