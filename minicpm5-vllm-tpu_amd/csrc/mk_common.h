@@ -104,6 +104,8 @@ __device__ inline void copy16_to_lds(const void* src, char* dst) {
 // that may go to LDS as well as memory, and while one is outstanding it makes every LDS read wait for
 // all earlier LDS reads (lgkmcnt(0)), which defeats operand prefetching; the buffer form is counted
 // by vmcnt alone.  Non-template for the same reason as copy16_to_lds.
+// Raw buffer resource over [base, base + bytes): stride 0, word 3 = 0x00020000 (32-bit data format,
+// the value gfx9-family raw buffer loads use; the format does not apply to untyped loads).
 __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
 }
