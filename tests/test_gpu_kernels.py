@@ -42,7 +42,7 @@ def _attn_inputs(B, S, hd, n_q=16, n_kv=2):
 
 @pytest.mark.parametrize("B,S,hd,theta", [(1, 256, 64, 1e4), (2, 512, 96, 1e4), (1, 1024, 128, 5e6),
                                            (3, 128, 128, 5e6), (2, 384, 96, 1e4), (1, 640, 128, 5e6),
-                                           (1, 8192, 96, 1e4), (1, 8192, 128, 5e6)])
+                                           (1, 8192, 96, 1e4), (1, 8192, 128, 5e6), (3, 2048, 128, 5e6)])
 def test_attention_vs_fp32(B, S, hd, theta):
     from minicpm5_mk import ops
     from minicpm5_mk.mk_weights import rope_tables
@@ -75,11 +75,12 @@ def test_attention_deterministic():
     assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("B,S,hd", [(2, 4096, 128), (4, 2048, 96)])
+@pytest.mark.parametrize("B,S,hd", [(2, 4096, 128), (4, 2048, 96), (3, 2048, 128)])
 def test_attention_batch_invariant(B, S, hd):
-    """Each sequence of a batch equals the same sequence run alone, bit for bit.  The batch launches
-    (B * 2 kv heads * S / 64 tile pairs = 256) take the static pair mapping, the single-sequence ones
-    the work queues, so this also checks that both mappings give identical results."""
+    """Each sequence of a batch equals the same sequence run alone, bit for bit.  (2, 4096) and
+    (4, 2048) launch 256 tile pairs (B * 2 kv heads * S / 64) and take the static pair mapping;
+    (3, 2048) launches 384 items on 256 persistent workgroups, so workgroups take several items and
+    drain the other kv head's queue; the single-sequence runs take the work queues one item each."""
     from minicpm5_mk import ops
     from minicpm5_mk.mk_weights import rope_tables
 
