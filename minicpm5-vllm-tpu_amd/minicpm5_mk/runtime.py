@@ -22,6 +22,13 @@ F32 = torch.float32
 WEIGHT_ORDER = ("w_qkv", "w_o", "w_gu", "w_down", "s_qkv", "s_o", "s_gu", "s_down",
                 "a_qkv", "a_o", "a_gu", "a_down", "wl_qkv", "wl_o", "wl_gu", "wl_down")
 ATTN_PREFIXES = ("auto", "v2", "super", "flash", "pallas", "splash", "xla")
+BF16_DUMMY = "bf16-dummy"      # (1,) or (L-1, 1): the unread scale slots of a bf16 linear
+
+
+def shape_ok(t: torch.Tensor, shape, Lm: int) -> bool:
+    if shape == BF16_DUMMY:
+        return tuple(t.shape) in ((1,), (Lm, 1))
+    return tuple(t.shape) == tuple(shape)
 
 
 def _stream():
@@ -29,7 +36,11 @@ def _stream():
 
 
 def expected_shapes(L: int, H: int, inter: int, n_q: int, n_kv: int, hd: int, quant: str) -> dict:
-    """{name: (shape, dtype)} of the reference-layout tensors (mk_weights.py:126-263) for `quant`."""
+    """{name: (shape, dtype)} of the reference-layout tensors (mk_weights.py:126-263) for `quant`.
+
+    The scales / activation factors of a bf16 linear are dummies that are never read: the reference
+    passes (1,) for an all-bf16 string (mk_weights.py:176-179) and (L-1, 1) for a bf16 linear of a
+    mixed string; their shape here is BF16_DUMMY, which accepts both."""
     qm = parse_quant(quant)
     fl = quant_flags(quant)
     Lm, qd = L - 1, n_q * hd
@@ -39,13 +50,13 @@ def expected_shapes(L: int, H: int, inter: int, n_q: int, n_kv: int, hd: int, qu
     wdt = {"bf16": BF16, "int8": torch.int8, "int8d": torch.int8, "fp8": torch.float8_e4m3fn,
            "fp8d": torch.float8_e4m3fn}
     wt = lambda k: wdt[qm[k]]  # noqa: E731
-    sc = lambda k, n: (Lm, n) if i8[k] else (Lm, 1)  # noqa: E731
+    sc = lambda k, n: (Lm, n) if i8[k] else BF16_DUMMY  # noqa: E731
     return {
         "w_qkv": ((Lm, H, D), wt("qkv")), "w_o": ((Lm, qd, H), wt("o")),
         "w_gu": ((Lm, H, 2 * inter) if fmlp else (Lm, H, 2, inter), wt("gu")),
         "w_down": ((Lm, inter, H), wt("down")),
         "s_qkv": (sc("qkv", D), F32), "s_o": (sc("o", H), F32),
-        "s_gu": (((Lm, 1, 2 * inter) if fmlp else (Lm, 2, inter)) if i8["gu"] else (Lm, 1), F32),
+        "s_gu": (((Lm, 1, 2 * inter) if fmlp else (Lm, 2, inter)) if i8["gu"] else BF16_DUMMY, F32),
         "s_down": (sc("down", H), F32),
         "a_qkv": (sc("qkv", H), F32), "a_o": (sc("o", qd), F32), "a_gu": (sc("gu", H), F32),
         "a_down": (sc("down", inter), F32),
@@ -69,7 +80,7 @@ class MkModel:
         exp = expected_shapes(L, H, inter, n_q, n_kv, head_dim, quant)
         for k, (shape, dtype) in exp.items():
             t = weights[k]
-            if tuple(t.shape) != tuple(shape) or t.dtype != dtype:
+            if not shape_ok(t, shape, L - 1) or t.dtype != dtype:
                 raise MkError(f"{k}: got {tuple(t.shape)} {t.dtype}, expected {shape} {dtype} for quant {quant!r}")
         others = {"embed": (embed, (V, H), BF16), "final_norm": (final_norm, (H,), BF16),
                   "cos": (cos, (cos.shape[0], head_dim), BF16), "sin": (sin, (cos.shape[0], head_dim), BF16)}

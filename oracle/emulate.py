@@ -286,6 +286,7 @@ def mk_forward(ids: torch.Tensor, w: dict, embed: torch.Tensor, final_norm: torc
     inter = cfg.inter
     x = embed[ids.long()].to(BF16).reshape(B * S, H)
     cos, sin = w["cos"], w["sin"]
+    w = {k: (t.expand(cfg.num_layers - 1, 1) if k[:2] in ("s_", "a_") and t.dim() == 1 else t) for k, t in w.items()}
     for l in range(cfg.num_layers - 1):
         if fqkv:
             qkv = fused_qkv(x, w["w_qkv"][l], w["s_qkv"][l], w["a_qkv"][l], eps)

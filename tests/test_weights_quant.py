@@ -2,7 +2,8 @@
 
 Pinned by invariants, not by restating the formulas:
   * per-output-channel int8: |dequant - w| <= scale / 2, scale = max(amax / 127, 1e-8), codes in +-127;
-  * SmoothQuant is exact algebra before rounding: (x diag(1/s)) (diag(s) W) == x W;
+  * calibration, SmoothQuant and quantisation against the reference's own outputs live in
+    tests/test_calib_fixture.py;
   * interleave_gu is a permutation with the [g_0 | u_0 | g_1 | u_1 ...] chunk order;
   * prepare_mk_weights' layout equals what the runtime (and libmk) expect for each quant string;
   * folding gamma / 1/sqrt(hd) is exact algebra: the bf16 path reproduces the FP32 model's q / k / v;
@@ -30,15 +31,6 @@ def test_quantize_w_bounds():
     assert (wq[:, 5] == 0).all() and float(s[5]) == float(torch.tensor(1e-8, dtype=torch.float32))
 
 
-def test_smoothquant_exact_algebra():
-    g = torch.Generator().manual_seed(1)
-    x = torch.randn(16, 64, generator=g, dtype=torch.float64)
-    w = torch.randn(64, 32, generator=g, dtype=torch.float64)
-    ax, aw = x.abs().amax(0), w.abs().amax(1)
-    s = (ax.pow(0.5) / aw.pow(0.5)).clamp(1e-4, 1e4)
-    assert torch.allclose((x / s) @ (s[:, None] * w), x @ w, rtol=1e-12, atol=1e-12)
-
-
 def test_interleave_gu_permutation():
     from minicpm5_mk.mk_weights import interleave_gu, mlp_chunk
 
@@ -62,7 +54,7 @@ def test_prepare_layout_matches_runtime(quant):
     from minicpm5_mk.config import preset
     from minicpm5_mk.mk_weights import prepare_mk_weights
     from minicpm5_mk.quant import resolve_quant_pair
-    from minicpm5_mk.runtime import expected_shapes
+    from minicpm5_mk.runtime import expected_shapes, shape_ok
     from minicpm5_mk.synth import random_hf_state_dict
 
     cfg = preset("tiny")
@@ -70,7 +62,7 @@ def test_prepare_layout_matches_runtime(quant):
     w = prepare_mk_weights(random_hf_state_dict(cfg), cfg.as_mk_cfg(), q, 512, log=lambda *a: None)
     for k, (shape, dtype) in expected_shapes(cfg.num_layers, cfg.hidden, cfg.inter, cfg.n_q, cfg.n_kv,
                                              cfg.head_dim, q).items():
-        assert tuple(w[k].shape) == tuple(shape) and w[k].dtype == dtype, (k, w[k].shape, w[k].dtype, shape, dtype)
+        assert shape_ok(w[k], shape, cfg.num_layers - 1) and w[k].dtype == dtype, (k, w[k].shape, w[k].dtype, shape)
     assert w["cos"].shape == (512, cfg.head_dim) and w["cos"].dtype == torch.bfloat16
 
 
@@ -100,13 +92,6 @@ def test_rope_tables_match_golden():
     cg, sg = golden.rope_tables(8192, 128, 5e6)
     # f32 angles rounded to bf16 vs f64 angles: one bf16 ulp plus the f32 angle error at t ~ 8k
     assert (c.float() - cg).abs().max() < 4e-3 and (s.float() - sg).abs().max() < 4e-3
-
-
-def test_calibration_ids_follow_reference_rng():
-    """_calibrate draws RandomState(seed).randint(1000, min(V, 30000), (n, s)) with position 0 = 1."""
-    ids = np.random.RandomState(42).randint(1000, 30000, size=(4, 128))
-    assert ids.shape == (4, 128) and ids.min() >= 1000 and ids.max() < 30000
-    assert ids[0, :3].tolist() == np.random.RandomState(42).randint(1000, 30000, size=3).tolist()
 
 
 def test_quant_grammar_and_auto():
