@@ -23,8 +23,8 @@ from dataclasses import dataclass, field
 
 import torch
 
-from . import sampling_fast_ok
 from .config import MkConfig, preset
+from .dispatch import StepView, eligible_step, mk_seq_ok
 from .mk_weights import prepare_mk_weights
 from .quant import resolve_quant_pair
 from .runtime import WEIGHT_ORDER, MkModel
@@ -81,28 +81,22 @@ class NotEligible(RuntimeError):
         self.reason = reason
 
 
-def mk_seq_ok(seq: int, max_seq: int) -> bool:
-    """The reference's fast-path length rule (model.py:131-136): <= 1024 -> multiple of 128, else of
-    1024 (libmk itself serves every multiple of 128)."""
-    if seq <= 0 or seq > max_seq:
-        return False
-    return seq % 128 == 0 if seq <= 1024 else seq % 1024 == 0
-
-
 def eligible_batch(prompts, sps, max_seq: int, require_mt1: bool = True):
-    """(bs, seq) iff the batch is one uniform fresh prefill the fast path serves, else NotEligible."""
-    lens = {len(p) for p in prompts}
-    if len(lens) != 1:
-        raise NotEligible("ragged", f"prompt lengths {sorted(lens)} differ")
-    seq = lens.pop()
-    for sp in sps:
-        if require_mt1 and (sp is None or sp.max_tokens != 1):
-            raise NotEligible("max_tokens", "only max_tokens == 1 requests are served")
-        if not sampling_fast_ok(sp):
-            raise NotEligible("unsupported_sampling_feature", "sampling feature outside the fast path")
-    if not mk_seq_ok(seq, max_seq):
-        raise NotEligible("seq", f"seq {seq} not served (multiple of 128, of 1024 above 1024, <= {max_seq})")
-    return len(prompts), seq
+    """(bs, seq) iff the batch is one uniform fresh prefill the fast path serves, else NotEligible with
+    the reference's reason code.  Every prompt here is a fresh, whole-prompt prefill (no KV cache
+    exists), so `continuation` and `partial_prefill` cannot occur; the same decision function serves
+    the vLLM runner hook (dispatch.eligible_step)."""
+    lens = [len(p) for p in prompts]
+    view = StepView(scheduled=lens, num_computed=[0] * len(lens), num_prompt=lens, sampling_params=list(sps),
+                    prompt_logprobs=[getattr(sp, "prompt_logprobs", None) is not None for sp in sps])
+    batch, reason = eligible_step(view, max_seq, require_mt1)
+    if batch is None:
+        raise NotEligible(reason, {"ragged": f"prompt lengths {sorted(set(lens))} differ",
+                                   "max_tokens": "only max_tokens == 1 requests are served",
+                                   "unsupported_sampling_feature": "sampling feature outside the fast path",
+                                   "seq": f"seq {lens[0] if lens else 0} not served (multiple of 128, of 1024 above "
+                                          f"1024, <= {max_seq})"}.get(reason, reason))
+    return batch
 
 
 class MkEngine:

@@ -1,20 +1,26 @@
 """vLLM model class: MiniCPM5 (Llama) whose uniform fresh prefill steps run through libmk.
 
 Mirrors plugin/minicpm5_mk/model.py (MiniCPM5MegakernelForCausalLM, :554-795): the stock
-LlamaForCausalLM is kept for every other step (decode, ragged or partial prefills); `load_weights`
-tees the HF tensors, prepares the plugin's quantized layout (prepare_mk_weights) and builds an
-`MkModel`; `forward` runs the fast path when the step is B equal-length sequences starting at
-position 0.  The reference returns (max(8, B), H) rows through a patched hidden-state selection
-(model.py:224-235); without runner patches this class scatters the B final-normed last-token rows
-to rows b*S + S - 1 of a (T, H) tensor (the reference's scatter_last, mk_jax.py:614-621), which is
-exactly what the stock logits selection reads.
+LlamaForCausalLM serves every other step (decode, chunked or partial prefills, ragged batches, dummy
+runs); `load_weights` tees the HF tensors, prepares the plugin's quantized layout
+(prepare_mk_weights) and builds an `MkModel`; `forward` runs the fast path when the host-side
+decision of this step says so.
+
+That decision is made before the forward from the scheduler's state, as the reference does
+(`_eligible_batch`, model.py:139-169): a hook on vLLM's GPU model runner (`dispatch.install_runner_hook`)
+checks that every request is a fresh, whole-prompt prefill of one length with max_tokens == 1 and no
+prompt logprobs, and records (bs, seq) or a reason code.  The forward never inspects device tensors.
+A fast-path prefill writes no KV cache, which is why max_tokens == 1 is required.  When the hook
+cannot be installed the fast path stays off.
+
+Without the reference's hidden-state selection patch (model.py:224-235) the forward returns a (T, H)
+tensor with the B final-normed last-token rows at rows b*S + S - 1, the rows the stock logits
+selection reads.
 
 Requires vLLM (imported at module import, like the reference).  Environment knobs kept from the
 reference (model.py:23-32): MINICPM5_MK_ENABLE, MINICPM5_MK_QUANT, MINICPM5_MK_ATTN,
-MINICPM5_MK_FREE_STOCK, MINICPM5_MK_LOG_EVERY, MINICPM5_MK_STATUS_DIR.  A fast-path prefill does
-not write vLLM's KV cache, so requests served by it must be max_tokens == 1 (the reference enforces
-this with TorchTPU runner hooks, model.py:139-525, which have no ROCm counterpart here); set
-MINICPM5_MK_ENABLE=0 for generation workloads.
+MINICPM5_MK_REQUIRE_MAX_TOKENS_1, MINICPM5_MK_FREE_STOCK, MINICPM5_MK_STATUS_DIR; and
+MINICPM5_MK_CHECK_POSITIONS=1 cross-checks each fast-path step against the device positions (syncs).
 """
 from __future__ import annotations
 
@@ -22,13 +28,14 @@ import json
 import logging
 import os
 import time
+import weakref
 from collections.abc import Iterable
 
 import torch
 from vllm.model_executor.models.llama import LlamaForCausalLM
 
 from .config import MkConfig
-from .engine import mk_seq_ok
+from .dispatch import STATE, install_runner_hook, positions_match, scatter_last_rows
 from .mk_weights import prepare_mk_weights
 from .quant import resolve_quant_pair
 from .runtime import WEIGHT_ORDER, MkModel
@@ -42,21 +49,15 @@ _WEIGHT_SUFFIXES = (
 )
 
 
-def uniform_prefill(positions: torch.Tensor):
-    """(B, S) iff positions are B copies of arange(S), else None (one host sync)."""
-    T = positions.numel()
-    if T == 0:
-        return None
-    pos = positions.reshape(-1)
-    zeros = torch.nonzero(pos == 0).reshape(-1)
-    if zeros.numel() == 0 or int(zeros[0]) != 0:
-        return None
-    S = int(zeros[1]) if zeros.numel() > 1 else T
-    if T % S:
-        return None
-    B = T // S
-    ok = torch.equal(pos, torch.arange(S, device=pos.device, dtype=pos.dtype).repeat(B))
-    return (B, S) if ok else None
+def _hook_vllm_runner(model) -> bool:
+    """Install the eligibility hook on vLLM's v1 GPU model runner (one class per process)."""
+    try:
+        from vllm.v1.worker.gpu_model_runner import GPUModelRunner
+    except ImportError:
+        return False
+    ref = weakref.ref(model)
+    require_mt1 = os.environ.get("MINICPM5_MK_REQUIRE_MAX_TOKENS_1", "1") != "0"
+    return install_runner_hook(GPUModelRunner, lambda runner: ref()._mk_max_seq if ref() else 0, require_mt1)
 
 
 class MiniCPM5MegakernelForCausalLM(LlamaForCausalLM):
@@ -81,6 +82,9 @@ class MiniCPM5MegakernelForCausalLM(LlamaForCausalLM):
             self._mk_cfg.validate()
         except ValueError as e:
             logger.warning("minicpm5_mk: %s; fast path disabled", e)
+            self._mk_enabled = False
+        if self._mk_enabled and not _hook_vllm_runner(self):
+            logger.warning("minicpm5_mk: vLLM GPU model runner not found; fast path disabled")
             self._mk_enabled = False
 
     def load_weights(self, weights: Iterable[tuple[str, torch.Tensor]]) -> set[str]:
@@ -134,20 +138,22 @@ class MiniCPM5MegakernelForCausalLM(LlamaForCausalLM):
         os.replace(path + ".tmp", path)
 
     def forward(self, input_ids, positions, intermediate_tensors=None, inputs_embeds=None):
-        if self._mk_model is not None and input_ids is not None and inputs_embeds is None and intermediate_tensors is None:
-            batch = uniform_prefill(positions)
-            if batch is not None and mk_seq_ok(batch[1], self._mk_max_seq):
-                B, S = batch
-                key = f"mk:{B}x{S}"
-                self._mk_counts["mk"] += 1
-                if key not in self._mk_counts:
-                    self._mk_counts[key] = 0
-                    self._mk_status["shapes"][key] = {"mode": "single", "quant": self._mk_model.quant}
-                    self._mk_write_status()
-                self._mk_counts[key] += 1
-                rows = self._mk_model.forward(input_ids.reshape(-1).to(torch.int32), B, S)[:B]
-                out = torch.zeros((input_ids.numel(), rows.shape[1]), dtype=rows.dtype, device=rows.device)
-                out.view(B, S, -1)[:, S - 1] = rows
-                return out
+        batch, reason = STATE.take()
+        if (batch is not None and self._mk_model is not None and input_ids is not None and inputs_embeds is None
+                and intermediate_tensors is None and batch[0] * batch[1] <= input_ids.numel()):
+            B, S = batch
+            if os.environ.get("MINICPM5_MK_CHECK_POSITIONS") == "1" and not positions_match(positions, B, S):
+                raise RuntimeError(f"minicpm5_mk: host decision {B}x{S} disagrees with the step's positions")
+            key = f"mk:{B}x{S}"
+            self._mk_counts["mk"] += 1
+            if key not in self._mk_counts:
+                self._mk_counts[key] = 0
+                self._mk_status["shapes"][key] = {"mode": "single", "quant": self._mk_model.quant}
+                self._mk_write_status()
+            self._mk_counts[key] += 1
+            rows = self._mk_model.forward(input_ids.reshape(-1)[: B * S].to(torch.int32), B, S)
+            return scatter_last_rows(rows, B, S, input_ids.numel())
         self._mk_counts["stock"] += 1
+        rkey = f"stock:{reason}"
+        self._mk_counts[rkey] = self._mk_counts.get(rkey, 0) + 1
         return super().forward(input_ids, positions, intermediate_tensors, inputs_embeds)

@@ -1,0 +1,196 @@
+"""Fast-path eligibility and row hand-back (minicpm5_mk.dispatch, minicpm5_mk.model), on the CPU.
+
+The decision mirrors the reference's `_eligible_batch` (plugin/minicpm5_mk/model.py:139-169): reason
+codes ragged, continuation, partial_prefill, max_tokens, unsupported_sampling_feature, checked in that
+order, plus the length rule `_mk_seq_ok` (:131-136).  The vLLM model class is exercised with test
+doubles for vLLM's LlamaForCausalLM and GPU model runner (vLLM is not installed here): a step the
+runner hook marks eligible goes to libmk's model object, every other step to the stock forward.
+"""
+import sys
+import types
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+from minicpm5_mk.dispatch import (STATE, StepView, eligible_step, install_runner_hook, mk_seq_ok, positions_match,
+                                  scatter_last_rows, step_view_from_runner)
+from minicpm5_mk.engine import SamplingParams
+
+SP1 = SamplingParams(max_tokens=1)
+
+
+def view(sched, computed=None, prompt=None, sps=None, plp=None):
+    n = len(sched)
+    return StepView(sched, computed if computed is not None else [0] * n, prompt if prompt is not None else list(sched),
+                    sps if sps is not None else [SP1] * n, plp if plp is not None else [False] * n)
+
+
+def test_eligible_and_reason_codes():
+    assert eligible_step(view([8192] * 4), 8256) == ((4, 8192), "ok")
+    assert eligible_step(view([1024]), 8256) == ((1, 1024), "ok")
+    assert eligible_step(view([]), 8256) == (None, "ragged")
+    assert eligible_step(view([8192, 4096]), 8256) == (None, "ragged")
+    assert eligible_step(view([8192, 8192], computed=[0, 5]), 8256) == (None, "continuation")
+    # chunked prefill: the first 2048-token chunk of a 10k prompt is not the whole prompt
+    assert eligible_step(view([2048], prompt=[10240]), 16384) == (None, "partial_prefill")
+    assert eligible_step(view([8192, 8192], sps=[SP1, SamplingParams(max_tokens=16)]), 8256) == (None, "max_tokens")
+    assert eligible_step(view([8192], sps=[None]), 8256) == (None, "max_tokens")
+    assert eligible_step(view([8192], sps=[SamplingParams(max_tokens=16)]), 8256, require_mt1=False) == ((1, 8192), "ok")
+    assert eligible_step(view([8192], sps=[SamplingParams(repetition_penalty=1.1)]), 8256) == \
+        (None, "unsupported_sampling_feature")
+    assert eligible_step(view([8192], plp=[True]), 8256) == (None, "unsupported_sampling_feature")
+    assert eligible_step(view([1000]), 8256) == (None, "seq")            # not a multiple of 128
+    assert eligible_step(view([1152]), 8256) == (None, "seq")            # above 1024: multiple of 1024 only
+    assert eligible_step(view([9216]), 8256) == (None, "seq")            # above max_seq
+
+
+def test_reason_order_follows_reference():
+    """A step that is both a continuation and max_tokens > 1 (decode) reports continuation first."""
+    v = view([1, 1], computed=[8192, 8192], prompt=[8192, 8192], sps=[SamplingParams(max_tokens=16)] * 2)
+    assert eligible_step(v, 8256) == (None, "continuation")
+    v = view([8192, 8192], computed=[8192, 8192], sps=[SamplingParams(max_tokens=16)] * 2)
+    assert eligible_step(v, 8256) == (None, "continuation")
+
+
+def test_mk_seq_ok_rule():
+    assert [mk_seq_ok(s, 8256) for s in (128, 384, 896, 1024, 1152, 2048, 3072, 8192, 9216, 0, -128)] == \
+        [True, True, True, True, False, True, True, True, False, False, False]
+
+
+def _fake_runner(req_ids, computed, prompt, sched, sps, plp=()):
+    n = len(req_ids)
+    ib = SimpleNamespace(num_reqs=n, req_ids=list(req_ids) + ["stale"],
+                         num_computed_tokens_cpu=np.array(list(computed) + [7], dtype=np.int32),
+                         num_prompt_tokens=np.array(list(prompt) + [3], dtype=np.int32))
+    runner = SimpleNamespace(input_batch=ib, requests={r: SimpleNamespace(sampling_params=sp) for r, sp in zip(req_ids, sps)},
+                             num_prompt_logprobs={r: 5 for r in plp})
+    so = SimpleNamespace(num_scheduled_tokens=dict(zip(req_ids, sched)))
+    return runner, so
+
+
+def test_step_view_from_runner():
+    runner, so = _fake_runner(["a", "b"], [0, 0], [8192, 8192], [8192, 8192], [SP1, SP1], plp=["b"])
+    v = step_view_from_runner(runner, so)
+    assert v.scheduled == [8192, 8192] and v.num_computed == [0, 0] and v.num_prompt == [8192, 8192]
+    assert v.prompt_logprobs == [False, True]
+    assert eligible_step(v, 8256) == (None, "unsupported_sampling_feature")
+    runner, so = _fake_runner(["a", "b"], [0, 0], [8192, 8192], [8192, 8192], [SP1, SP1])
+    assert eligible_step(step_view_from_runner(runner, so), 8256) == ((2, 8192), "ok")
+
+
+def test_runner_hook_records_decision():
+    calls = []
+
+    class Runner:
+        def _prepare_inputs(self, scheduler_output):
+            calls.append("prep")
+            return "prepared"
+
+        def _dummy_run(self, n):
+            calls.append("dummy")
+            return n
+
+    runner, so = _fake_runner(["a"], [0], [4096], [4096], [SP1])
+    r = Runner()
+    r.__dict__.update(runner.__dict__)
+    assert install_runner_hook(Runner, lambda rr: 8256) and install_runner_hook(Runner, lambda rr: 8256)
+    assert r._prepare_inputs(so) == "prepared" and calls == ["prep"]       # wrapped once
+    assert STATE.take() == ((1, 4096), "ok")
+    assert STATE.take() == (None, "ok")                                    # one forward per decision
+    r.input_batch.num_computed_tokens_cpu[0] = 4096
+    r._prepare_inputs(so)
+    assert STATE.take() == (None, "continuation")
+    r._dummy_run(8)
+    assert STATE.take() == (None, "dummy")
+    # a runner layout the hook cannot read falls back to the stock path with a reason
+    bad = Runner()
+    bad._prepare_inputs(SimpleNamespace())
+    b, reason = STATE.take()
+    assert b is None and reason.startswith("check_error")
+
+
+def test_scatter_last_rows_and_positions():
+    rows = torch.arange(8 * 4, dtype=torch.float32).view(8, 4)            # (max(8, B), H) with B = 3
+    out = scatter_last_rows(rows, 3, 5, 17)
+    assert out.shape == (17, 4)
+    want = torch.zeros(17, 4)
+    for b in range(3):
+        want[b * 5 + 4] = rows[b]
+    assert torch.equal(out, want)
+    with pytest.raises(ValueError):
+        scatter_last_rows(rows, 4, 5, 17)
+    pos = torch.arange(5).repeat(3)
+    assert positions_match(pos, 3, 5) and not positions_match(pos, 5, 3) and not positions_match(pos, 4, 5)
+    assert positions_match(torch.cat([pos, torch.zeros(2, dtype=pos.dtype)]), 3, 5)
+
+
+@pytest.fixture
+def fake_vllm(monkeypatch):
+    """Minimal stand-ins for the two vLLM classes minicpm5_mk.model touches (test doubles)."""
+    class LlamaForCausalLM(torch.nn.Module):
+        def __init__(self, *, vllm_config, prefix=""):
+            super().__init__()
+            self.stock_calls = 0
+
+        def forward(self, input_ids, positions, intermediate_tensors=None, inputs_embeds=None):
+            self.stock_calls += 1
+            return "stock"
+
+    class GPUModelRunner:
+        def _prepare_inputs(self, scheduler_output):
+            return None
+
+    mods = {
+        "vllm": types.ModuleType("vllm"),
+        "vllm.model_executor": types.ModuleType("vllm.model_executor"),
+        "vllm.model_executor.models": types.ModuleType("vllm.model_executor.models"),
+        "vllm.model_executor.models.llama": types.ModuleType("vllm.model_executor.models.llama"),
+        "vllm.v1": types.ModuleType("vllm.v1"),
+        "vllm.v1.worker": types.ModuleType("vllm.v1.worker"),
+        "vllm.v1.worker.gpu_model_runner": types.ModuleType("vllm.v1.worker.gpu_model_runner"),
+    }
+    mods["vllm.model_executor.models.llama"].LlamaForCausalLM = LlamaForCausalLM
+    mods["vllm.v1.worker.gpu_model_runner"].GPUModelRunner = GPUModelRunner
+    for k, m in mods.items():
+        monkeypatch.setitem(sys.modules, k, m)
+    monkeypatch.delitem(sys.modules, "minicpm5_mk.model", raising=False)
+    import minicpm5_mk.model as model_mod
+    yield model_mod, GPUModelRunner
+    sys.modules.pop("minicpm5_mk.model", None)
+
+
+def test_model_class_dispatch(fake_vllm):
+    model_mod, Runner = fake_vllm
+    hf = dict(hidden_size=256, num_attention_heads=16, num_key_value_heads=2, head_dim=64, num_hidden_layers=3,
+              intermediate_size=768, vocab_size=32768, rms_norm_eps=1e-6, rope_theta=1e4)
+    cfg = SimpleNamespace(model_config=SimpleNamespace(hf_config=SimpleNamespace(**hf), max_model_len=8256),
+                          parallel_config=SimpleNamespace(pipeline_parallel_size=1, tensor_parallel_size=1))
+    m = model_mod.MiniCPM5MegakernelForCausalLM(vllm_config=cfg)
+    assert m._mk_enabled and getattr(Runner, "_minicpm5_mk_hooked", False)
+
+    class FakeMk:
+        quant = "int8d"
+
+        def __init__(self):
+            self.calls = []
+
+        def forward(self, ids, bs, seq):
+            self.calls.append((ids.dtype, ids.numel(), bs, seq))
+            return torch.arange(8 * 4, dtype=torch.float32).view(8, 4) + 1
+
+    m._mk_model, m._mk_status = FakeMk(), {"shapes": {}}
+    ids = torch.arange(2 * 128 + 16)                                         # padded: T_pad > bs * seq
+    pos = torch.cat([torch.arange(128).repeat(2), torch.zeros(16, dtype=torch.long)])
+    STATE.set((2, 128), "ok")
+    out = m(ids, pos)
+    assert m._mk_model.calls == [(torch.int32, 256, 2, 128)]
+    assert out.shape == (272, 4) and torch.equal(out[127], torch.arange(4.0) + 1) and torch.equal(out[255], torch.arange(4.0) + 5)
+    assert float(out.abs().sum()) == float(out[127].sum() + out[255].sum())
+    STATE.set(None, "continuation")
+    assert m(ids, pos) == "stock" and m._mk_counts["stock:continuation"] == 1
+    assert m(ids, pos) == "stock"                                            # no decision recorded: stock
+    STATE.set((4, 128), "ok")                                                # more tokens than the step holds
+    assert m(ids, pos) == "stock"
+    assert m._mk_counts["mk"] == 1 and m._mk_counts["mk:2x128"] == 1
