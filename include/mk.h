@@ -30,7 +30,7 @@ extern "C" {
 #define MK_OK 0
 #define MK_EINVAL -1       /* bad shape / argument / quant string           */
 #define MK_EHIP -2         /* a HIP runtime call failed                       */
-#define MK_EUNSUPPORTED -3 /* valid for the reference, not built here (fp8)   */
+#define MK_EUNSUPPORTED -3 /* valid for the reference, not built here          */
 #define MK_ENOMEM -4       /* caller-provided buffer too small                */
 
 /* Model dimensions: the reference's _mk_cfg (model.py:561-567) plus vocab and RoPE table rows. */
@@ -53,7 +53,8 @@ typedef struct mk_config {
  *   w_gu  (L-1, H, 2I) chunk-interleaved [g_c | u_c] (flag fmlp) or (L-1, H, 2, I), int8 or bf16;
  *   w_down(L-1, I, H)                   int8 or bf16;
  *   s_* (L-1, out) f32 per-output-channel scales (s_gu (L-1, 1, 2I) in w_gu's column order);
- *   a_* (L-1, in) f32 per-input-channel activation factors;  bf16 linears pass (L-1, 1) dummies;
+ *   a_* (L-1, in) f32 per-input-channel activation factors;  bf16 linears pass unread (1,) or (L-1, 1)
+ *   dummies;
  *   wl_qkv (H, D), wl_o (q_dim, H), wl_gu (H, 2, I), wl_down (I, H) bf16 (last layer, gamma folded);
  *   lm_head (V, H) bf16 (HF layout), optional: NULL means no logits. */
 typedef struct mk_weights {
@@ -89,7 +90,8 @@ int mk_abi_version(void);
 
 /* Host-only validation of a config / quant string / (bs, seq) without touching the GPU.
  * Mirrors the reference's trace-time asserts (mk_attn.py:672-673, mk_mlp.py:119,185) and the fast-path
- * length rule _mk_seq_ok (model.py:131-136) restricted to what the kernels support (seq % 256 == 0). */
+ * length rule _mk_seq_ok (model.py:131-136) widened to what the kernels serve: every seq that is a
+ * positive multiple of 128 and <= max_seq. */
 int mk_validate(const mk_config* cfg, const char* quant, int bs, int seq);
 
 /* Bytes of the packed-weight buffer mk_model_create needs (host-only). */
@@ -145,7 +147,8 @@ int mk_forward_timed(mk_model* m, const int32_t* input_ids, int bs, int seq, voi
  * -> out (B, S, n_q hd) bf16, RoPE from the bf16 cos / sin tables applied in-kernel, softmax in f32
  * with scores scaled by sm_scale (pass 1.0 when 1/sqrt(hd) is folded into W_q, as the plugin does).
  * scratch: mk_attn_scratch_bytes(B, S, n_kv, hd) bytes (RoPE'd K, V transposed, and one work-queue counter per
- * kv head, so n_kv <= 63); calls that share one scratch buffer must not overlap. */
+ * kv head, so n_kv <= 63); calls that share one scratch buffer must not overlap.  qkv, cos, sin, out and
+ * scratch must be 16-byte aligned (MK_EINVAL otherwise); cos / sin hold >= S rows; S <= 131072. */
 size_t mk_attn_scratch_bytes(int B, int S, int n_kv, int head_dim);
 int mk_attn_prefill(const void* qkv, const void* cos, const void* sin, void* out, void* scratch,
                     size_t scratch_bytes, int B, int S, int n_q, int n_kv, int head_dim, float sm_scale,

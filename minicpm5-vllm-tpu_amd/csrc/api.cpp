@@ -131,6 +131,11 @@ int mk_set_graph_mode(mk_model* m, int enable) {
   return MK_OK;
 }
 
+namespace {
+// the attention kernels move qkv, the RoPE tables, the scratch and the output in 16-byte vectors
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+}  // namespace
+
 size_t mk_attn_scratch_bytes(int B, int S, int n_kv, int head_dim) {
   return mk::attn_scratch_bytes(B, S, n_kv, head_dim);
 }
@@ -141,6 +146,8 @@ int mk_attn_prefill(const void* qkv, const void* cos, const void* sin, void* out
   int rc = mk::attn_validate(B, S, n_q, n_kv, head_dim);
   if (rc) return rc;
   MK_REQUIRE(qkv && cos && sin && out && scratch, "attn_prefill: null pointer");
+  MK_REQUIRE(aligned16(qkv) && aligned16(cos) && aligned16(sin) && aligned16(out) && aligned16(scratch),
+             "attn_prefill: qkv, cos, sin, out and scratch must be 16-byte aligned");
   MK_REQUIRE(scratch_bytes >= mk::attn_scratch_bytes(B, S, n_kv, head_dim), "attn_prefill: scratch too small");
   MK_REQUIRE(sm_scale > 0.f, "attn_prefill: sm_scale must be > 0");
   mk::AttnArgs a{};
@@ -166,6 +173,8 @@ int mk_bench_attn(const void* qkv, const void* cos, const void* sin, void* out, 
   int rc = mk::attn_validate(B, S, n_q, n_kv, head_dim);
   if (rc) return rc;
   MK_REQUIRE(qkv && cos && sin && out && scratch, "bench_attn: null pointer");
+  MK_REQUIRE(aligned16(qkv) && aligned16(cos) && aligned16(sin) && aligned16(out) && aligned16(scratch),
+             "bench_attn: qkv, cos, sin, out and scratch must be 16-byte aligned");
   MK_REQUIRE(scratch_bytes >= mk::attn_scratch_bytes(B, S, n_kv, head_dim), "bench_attn: scratch too small");
   mk::AttnArgs a{};
   a.qkv = static_cast<const uint16_t*>(qkv);

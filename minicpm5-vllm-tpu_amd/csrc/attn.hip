@@ -743,6 +743,8 @@ int launch_last_attn_hd(const LastAttnArgs& a, hipStream_t st) {
 int attn_validate(int B, int S, int n_q, int n_kv, int hd) {
   MK_REQUIRE(B >= 1, "attention: batch must be >= 1");
   MK_REQUIRE(S >= 64 && S % 64 == 0, "attention: seq must be a positive multiple of 64");
+  // one (sequence, kv head) slice of K or V^T is addressed through a 32-bit buffer resource
+  MK_REQUIRE(S <= 131072, "attention: seq must be <= 131072");
   MK_REQUIRE(n_kv >= 1 && n_q == G * n_kv, "attention: n_q must equal 8 * n_kv (GQA group of 8)");
   MK_REQUIRE(n_kv <= 63, "attention: at most 63 kv heads (one work-queue counter each)");
   MK_REQUIRE(hd == 64 || hd == 96 || hd == 128, "attention: head_dim must be 64, 96 or 128");

@@ -139,3 +139,31 @@ def test_attn_prefill_rejects_before_launch(B, S, n_q, n_kv, hd, msg):
     rc = lib.mk_attn_prefill(None, None, None, None, None, 0, B, S, n_q, n_kv, hd, 1.0, None)
     assert rc != 0
     assert msg in lib.mk_last_error().decode()
+
+
+@pytest.mark.parametrize("bad", ["qkv", "cos", "sin", "out", "scratch"])
+def test_attn_prefill_rejects_misaligned_pointers(bad):
+    """The attention kernels move 16-byte vectors: a misaligned pointer is MK_EINVAL before any launch
+    (the pointers here are never dereferenced)."""
+    from minicpm5_mk import _lib
+
+    lib = _lib.load()
+    ptr = {k: ctypes.c_void_p(0x10000 * (i + 1)) for i, k in enumerate(("qkv", "cos", "sin", "out", "scratch"))}
+    ptr[bad] = ctypes.c_void_p(ptr[bad].value + 8)
+    need = lib.mk_attn_scratch_bytes(1, 1024, 2, 128)
+    rc = lib.mk_attn_prefill(ptr["qkv"], ptr["cos"], ptr["sin"], ptr["out"], ptr["scratch"], need, 1, 1024, 16, 2,
+                             128, ctypes.c_float(1.0), None)
+    assert rc == -1 and b"16-byte aligned" in lib.mk_last_error()
+    avg = ctypes.c_float()
+    rc = lib.mk_bench_attn(ptr["qkv"], ptr["cos"], ptr["sin"], ptr["out"], ptr["scratch"], need, 1, 1024, 16, 2, 128,
+                           ctypes.c_float(1.0), 1, None, ctypes.byref(avg))
+    assert rc == -1 and b"16-byte aligned" in lib.mk_last_error()
+
+
+def test_attn_prefill_rejects_oversized_seq():
+    from minicpm5_mk import _lib
+
+    lib = _lib.load()
+    p = ctypes.c_void_p(0x10000)
+    rc = lib.mk_attn_prefill(p, p, p, p, p, 1 << 40, 1, 262144, 16, 2, 128, ctypes.c_float(1.0), None)
+    assert rc == -1 and b"131072" in lib.mk_last_error()
