@@ -17,9 +17,13 @@ Extra fields:
   kernels       the same for every kernel category: QKV / gate-up GEMMs (int8 MFMA, peak 5.0 POP/s when
                 quantised), O / down (bf16 unless quantised), the row kernels and the LM head (HBM GB/s).
   cpu_baseline  the oracle's FP32 CPU forward (oracle/golden.py, a restatement of the reference's
-                FP32 golden) timed on a bounded sample -- the first --cpu-layers layers of one
-                8192-token sequence -- and scaled to the full model (layers + LM head).
-  sweep         with --sweep: tokens/s and p50 at the other (B, 8192) shapes.
+                FP32 golden) of one whole 8192-token sequence of the main architecture with every host
+                thread: one warm-up of the first layer, then --cpu-runs timed full forwards (median).
+  sweep         the metric's other points: tokens/s, mean and p50 latency at (B, 8192) for each
+                (architecture, B) of --sweep (default: 1B at B = 4..32, 2B at B = 1..32, 1B-hd96 at B = 1),
+                each with `roofline_ms`, the whole model's bound at MI355X's published peaks (every linear
+                at its operand type's dense MFMA peak, causal attention at the bf16 peak, the LM head's
+                weight read at HBM bandwidth), and `frac_roofline` = roofline_ms / mean latency.
 """
 from __future__ import annotations
 
@@ -36,8 +40,9 @@ sys.path[:0] = [ROOT, os.path.join(ROOT, "minicpm5-vllm-tpu_amd")]
 PEAK = {"bf16": 2516.6, "int8": 5033.2, "fp8": 5033.2, "hbm": 8000.0}   # MI355X dense TFLOP/s, TOP/s; HBM GB/s
 METRIC = "prefill tokens/sec at (B,8192) B=1..32, 1B and 2B arch; p50 ms at (1,8192)"
 # HBM bytes per attn_fwd_kernel launch measured by rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (scaled by a
-# 256 MiB copy's counters) for the default workload; profiles/mfma_util_hbm_1b_b1_s8192.txt
-ATTN_TRAFFIC = {("1b", 1, 8192, "auto"): (77.1e6 + 33.6e6)}
+# 256 MiB copy's counters) for the default workload; (arch, B, S, quant) -> (bytes, source file)
+ATTN_TRAFFIC = {("1b", 1, 8192, "auto"): (77.1e6 + 33.6e6, "profiles/mfma_util_hbm_1b_b1_s8192.txt")}
+DEFAULT_SWEEP = "1b:4,8,16,32;2b:1,4,8,16,32;1b-hd96:1"
 
 
 def log(*a):
@@ -63,6 +68,25 @@ def flops_reference(cfg, bs, seq):
     lin = 2 * (qkv + o + gu + dn) * cfg.num_layers * bs * seq
     attn = cfg.num_layers * bs * 2 * seq * seq * cfg.head_dim * cfg.n_q
     return lin + attn + 2 * cfg.hidden * cfg.vocab * bs
+
+
+def roofline_ms(cfg, quant, bs, seq):
+    """Lower bound of one (bs, seq) prefill at MI355X's published peaks: the plugin's actual work --
+    L-1 full-sequence layers (each linear at its operand type's dense MFMA peak, causal attention
+    4 hd n_q S(S+1)/2 at the bf16 peak), the last layer's K/V projection over S tokens (bf16), and the
+    LM head's bf16 weight read at HBM bandwidth; the last-token GEMVs are negligible."""
+    from minicpm5_mk.quant import parse_quant
+
+    qm = parse_quant(quant)
+    T = bs * seq
+    H, I, hd, nq, nkv = cfg.hidden, cfg.inter, cfg.head_dim, cfg.n_q, cfg.n_kv
+    lin = {"qkv": 2.0 * T * H * (nq + 2 * nkv) * hd, "o": 2.0 * T * nq * hd * H, "gu": 2.0 * T * H * 2 * I,
+           "down": 2.0 * T * I * H}
+    peak = lambda k: PEAK["bf16" if qm[k] == "bf16" else "int8"] * 1e12  # noqa: E731
+    layer = sum(f / peak(k) for k, f in lin.items()) + 4.0 * hd * nq * seq * (seq + 1) / 2 * bs / (PEAK["bf16"] * 1e12)
+    last = 2.0 * T * H * 2 * nkv * hd / (PEAK["bf16"] * 1e12)
+    head = 2.0 * cfg.vocab * H / (PEAK["hbm"] * 1e9)
+    return ((cfg.num_layers - 1) * layer + last + head) * 1e3
 
 
 def time_steps(eng, ids, steps, warmup):
@@ -210,35 +234,33 @@ def attainable_peaks(iters=3000):
     return out
 
 
-def cpu_baseline(cfg, n_layers, seq=8192):
-    """The oracle's FP32 forward (restating benchmark/f32_golden.py) on `n_layers` layers of one
-    sequence, scaled to the full model: layers x L / n_layers + the LM head."""
+def cpu_baseline(cfg, runs, seq=8192):
+    """The oracle's FP32 forward (restating benchmark/f32_golden.py) of one whole `seq`-token sequence
+    with every host thread: one untimed warm-up over the first layer, then `runs` timed full forwards
+    (embedding, all L layers, final norm, LM head); value = seq / median time."""
     import torch
 
     from minicpm5_mk.synth import random_hf_state_dict, random_token_ids
     from oracle import golden
 
     torch.set_num_threads(os.cpu_count() or 1)
-    names = {"model.embed_tokens.weight", "model.norm.weight", "lm_head.weight"}
-    sub = cfg.replace(num_layers=n_layers)
-    for i in range(n_layers):
-        p = f"model.layers.{i}."
-        names |= {p + n for n in ("input_layernorm.weight", "post_attention_layernorm.weight", "self_attn.q_proj.weight",
-                                  "self_attn.k_proj.weight", "self_attn.v_proj.weight", "self_attn.o_proj.weight",
-                                  "mlp.gate_proj.weight", "mlp.up_proj.weight", "mlp.down_proj.weight")}
-    sd = random_hf_state_dict(cfg, names=names)
-    W = golden.load_f32(sd, sub)
-    del sd
+    t0 = time.perf_counter()
+    W = golden.load_f32(random_hf_state_dict(cfg), cfg)
+    t_load = time.perf_counter() - t0
     ids = random_token_ids(1, seq)[0]
     cos, sin = golden.rope_tables(seq, cfg.head_dim, cfg.rope_theta)
-    t0 = time.perf_counter()
-    golden.forward_one(ids, W, sub, cos, sin)
-    t_sample = time.perf_counter() - t0
-    t_full = t_sample * cfg.num_layers / n_layers
-    return {"value": seq / t_full, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"oracle FP32 forward (oracle/golden.py) of layers 0..{n_layers - 1} + final norm + LM head "
-                      f"of one {seq}-token sequence in {t_sample:.1f}s, scaled x{cfg.num_layers}/{n_layers} "
-                      f"-> {t_full:.1f}s per sequence",
+    golden.forward_one(ids, W, cfg.replace(num_layers=1), cos, sin)      # warm-up: one layer
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        golden.forward_one(ids, W, cfg, cos, sin)
+        times.append(time.perf_counter() - t0)
+    med = pctl(times, 50)
+    return {"value": round(seq / med, 1), "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"oracle FP32 forward (oracle/golden.py) of one whole {seq}-token sequence of {cfg.name} "
+                      f"({cfg.num_layers} layers + final norm + LM head), {runs} timed runs after a one-layer "
+                      f"warm-up: {', '.join(f'{t:.1f}' for t in times)} s (median {med:.1f} s); weights "
+                      f"generated and upcast in {t_load:.1f} s (untimed)",
             "cpu_model": _cpu_model()}
 
 
@@ -262,8 +284,10 @@ def main():
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--seq", type=int, default=8192)
     ap.add_argument("--quant", default="auto")
-    ap.add_argument("--sweep", default="", help="extra batch sizes, e.g. 4,8,16,32")
-    ap.add_argument("--cpu-layers", type=int, default=2, help="layers in the CPU-baseline sample (0 = skip)")
+    ap.add_argument("--sweep", default=DEFAULT_SWEEP,
+                    help="extra (architecture, batch) rows: 'arch:B,B;arch:B' ('B,B' = the --arch architecture; "
+                         "'' = none)")
+    ap.add_argument("--cpu-runs", type=int, default=2, help="timed full CPU forwards of the baseline (0 = skip)")
     ap.add_argument("--no-kernels", action="store_true")
     ap.add_argument("--kernels-only", action="store_true",
                     help="only the per-kernel timing loops + a 256 MiB device copy (rocprofv3 --pmc calibration)")
@@ -280,6 +304,7 @@ def main():
     from minicpm5_mk.synth import random_token_ids
 
     cfg = preset(args.arch)
+    main_arch = args.arch
     if args.kernels_only:
         src = torch.ones(64 << 20, dtype=torch.float32, device="cuda:0")   # 256 MiB read + 256 MiB written
         dst = torch.empty_like(src)
@@ -292,16 +317,18 @@ def main():
     eng = MkEngine(cfg, quant=args.quant, max_model_len=max(8256, args.seq + 64), log=log)
     log(f"[bench] engine built in {time.perf_counter() - t0:.1f}s quant={eng.quant}")
 
-    def run(B, steps, warmup):
+    def run(eng, c, B, steps, warmup):
         ids = random_token_ids(B, args.seq, seed=1234).to("cuda:0")
         wall, lat = time_steps(eng, ids, steps, warmup)
         mean = sum(lat) / len(lat)
-        return {"batch": B, "tokens_per_s": B * args.seq / (mean / 1e3), "mean_ms": mean, "p50_ms": pctl(lat, 50),
-                "p90_ms": pctl(lat, 90), "wall_ms_per_step": wall,
-                "tflops_reference_formula": flops_reference(cfg, B, args.seq) / (mean / 1e3) / 1e12}
+        bound = roofline_ms(c, eng.quant, B, args.seq)
+        return {"arch": c.name, "batch": B, "tokens_per_s": B * args.seq / (mean / 1e3), "mean_ms": mean,
+                "p50_ms": pctl(lat, 50), "p90_ms": pctl(lat, 90), "wall_ms_per_step": wall, "steps": steps,
+                "roofline_ms": bound, "frac_roofline": bound / mean,
+                "tflops_reference_formula": flops_reference(c, B, args.seq) / (mean / 1e3) / 1e12}
 
-    main_run = run(args.batch, args.steps, args.warmup)
-    log(f"[bench] B={args.batch}: {main_run}")
+    main_run = run(eng, cfg, args.batch, args.steps, args.warmup)
+    log(f"[bench] {cfg.name} B={args.batch}: {main_run}")
     kern = attain = None
     if not args.no_kernels:
         kern = model_roofline(eng, cfg, random_token_ids(args.batch, args.seq, seed=1234).to("cuda:0"))
@@ -313,16 +340,34 @@ def main():
                 ap_ = attain["bf16" if e["unit"] == "TFLOP/s" else "int8"]["rate"]
                 e["attainable"] = ap_
                 e["frac_attainable"] = round(e["achieved"] / ap_, 4)
+    rows = {}
+    for part in [p for p in (args.sweep or "").split(";") if p.strip()]:
+        arch, bs = part.split(":", 1) if ":" in part else (args.arch, part)
+        rows.setdefault(arch.strip(), []).extend(int(x) for x in bs.split(",") if x.strip())
     sweep = []
-    for b in [int(x) for x in args.sweep.split(",") if x.strip()]:
-        r = run(b, max(3, min(args.steps, int(80 / b))), 1)
-        log(f"[bench] sweep B={b}: {r}")
-        sweep.append(r)
+    for arch, batches in rows.items():
+        if arch != args.arch:
+            eng.model.release_buffers()
+            eng.close()
+            del eng
+            torch.cuda.empty_cache()
+            c = preset(arch)
+            t0 = time.perf_counter()
+            eng = MkEngine(c, quant=args.quant, max_model_len=max(8256, args.seq + 64), log=log)
+            log(f"[bench] {arch} engine built in {time.perf_counter() - t0:.1f}s quant={eng.quant}")
+            args.arch, cfg_now = arch, c
+        else:
+            cfg_now = preset(arch)
+        for b in batches:
+            r = run(eng, cfg_now, b, max(3, min(args.steps, int(80 / b))), 1)
+            log(f"[bench] sweep {arch} B={b}: {r}")
+            sweep.append(r)
+            eng.model.release_buffers()
     eng.model.release_buffers()
     eng.close()
     del eng
     torch.cuda.empty_cache()
-    cpu = cpu_baseline(cfg, args.cpu_layers, args.seq) if args.cpu_layers > 0 else None
+    cpu = cpu_baseline(cfg, args.cpu_runs, args.seq) if args.cpu_runs > 0 else None
     if cpu:
         log(f"[bench] cpu baseline: {cpu}")
 
@@ -332,16 +377,21 @@ def main():
         "p50_ms": round(main_run["p50_ms"], 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "int8+bf16" if args.quant != "bf16" else "bf16",
         "data": "synthetic: random-init N(0,0.02) weights (seed 0), token ids U[1000,30000) (seed 1234)",
-        "config": {"workload": f"minicpm5-{args.arch} prefill/scoring ({args.batch},{args.seq}), last-token logits",
+        "config": {"workload": f"{cfg.name} prefill/scoring ({args.batch},{args.seq}), last-token logits",
                    "arch": cfg.name, "batch": args.batch, "seq_len": args.seq, "head_dim": cfg.head_dim,
                    "quant": args.quant, "parallelism": "single GPU"},
         "tflops_reference_formula": round(main_run["tflops_reference_formula"], 1),
+        "roofline_ms": round(main_run["roofline_ms"], 3), "frac_roofline": round(main_run["frac_roofline"], 4),
     }
     if kern:
         a = kern["attn"]
+        traffic = ATTN_TRAFFIC.get((main_arch, args.batch, args.seq, args.quant))
         out["roofline"] = {"bound": "mfma", "achieved": a["achieved"], "peak": a["peak"], "unit": a["unit"],
                            "frac": a["frac"],
-                           "traffic": ATTN_TRAFFIC.get((args.arch, args.batch, args.seq, args.quant)),
+                           "traffic": traffic[0] if traffic else None,
+                           "traffic_source": (f"{traffic[1]}: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of this "
+                                              "workload, scaled by a 256 MiB copy's counters") if traffic else
+                           "not measured for this workload",
                            "kernel": "attn_fwd_kernel",
                            "avg_ms": round(a["avg_us"] / 1e3, 4), "timing": "in-model, HIP events per launch",
                            "attainable": {"peak": attain["bf16"]["rate"], "frac": a["frac_attainable"],
