@@ -154,6 +154,16 @@ int mk_attn_prefill(const void* qkv, const void* cos, const void* sin, void* out
                     size_t scratch_bytes, int B, int S, int n_q, int n_kv, int head_dim, float sm_scale,
                     void* stream);
 
+/* No counterpart in the reference: mk_attn_prefill for callers that cannot allocate device memory (code
+ * under hipGraph capture, tight serving loops, harnesses that forbid hipMalloc).  Same kernels and
+ * result; the scratch is a file-scope device array of MK_NOALLOC_SCRATCH_BYTES that every GPU the
+ * library runs on holds until the process ends, so B * S * n_kv * head_dim * 4 + 256 must not exceed it
+ * (MK_ENOMEM otherwise; 40 MiB = five 8192-token sequences at n_kv 2, hd 128).  Allocates nothing.
+ * Calls that overlap on one GPU race on its array. */
+#define MK_NOALLOC_SCRATCH_BYTES ((size_t)40 << 20)
+int mk_attn_prefill_noalloc(const void* qkv, const void* cos, const void* sin, void* out, int B, int S, int n_q,
+                            int n_kv, int head_dim, float sm_scale, void* stream);
+
 /* Per-token dynamic int8 quantisation of rows x (T, H) (bf16, or f32 when x_f32):
  *   norm:  rstd = rsqrt(mean(x^2) + eps), else 1;  u = x * a (a NULL = ones);
  *   s = max(amax|u| / 127, 1e-6);  q = round_half_even(u * (1/s)) (fused: recip = 1) or u / s;

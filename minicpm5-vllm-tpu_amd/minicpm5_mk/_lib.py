@@ -55,6 +55,7 @@ SIGNATURES = {
     "mk_forward_timed": (_I, [_P, _P, _I, _I, _P, _P, _P, _SZ, _P, _P, _P]),
     "mk_attn_scratch_bytes": (_SZ, [_I, _I, _I, _I]),
     "mk_attn_prefill": (_I, [_P, _P, _P, _P, _P, _SZ, _I, _I, _I, _I, _I, _F, _P]),
+    "mk_attn_prefill_noalloc": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P]),
     "mk_row_quant": (_I, [_P, _I, _P, _I, _I, _F, _I, _I, _P, _P, _P]),
     "mk_act_quant": (_I, [_P, _I, _P, _I, _I, _F, _I, _I, _P, _P, _P]),
     "mk_mfma_peak_scratch_bytes": (_SZ, [_I]),
