@@ -222,6 +222,18 @@ int mk_gemm(int in_type, int epi, const void* A, int lda, const void* B, int ldb
 /* Last-token LM head: logits (B, V) f32 = hidden (B, H) bf16 @ lm_head (V, H)^T, any B. */
 int mk_lm_head(const void* hidden, const void* lm_head, int B, int H, int V, float* logits, void* stream);
 
+/* Weight preparation on the GPU: the per-parameter work of prepare_mk_weights (mk_weights.py:113-123,
+ * :229-252), bit-identical to the CPU restatement; the small FP32 calibration forward stays on the host.
+ * w is an HF linear weight (n_out, n_in) bf16 and W = w^T * fold its (in, out) f32 view (fold = 1/sqrt(hd)
+ * for the q projection, mk_weights.py:147, else 1).
+ *   mk_weight_row_amax: amax[j] = max_n |W[j, n]|, the weight statistic of SmoothQuant's factors;
+ *   mk_weight_quantize: v = W[j, n] * smooth[j] (smooth NULL = ones), scale[n] = max(max_j |v| / qmax, 1e-8)
+ *     into scale_ws (n_out floats), codes[j * ld_codes + n] = clamp(round_half_even(v / scale), +-127) (int8)
+ *     or e4m3(clamp(v / scale, +-448)) (fp8 != 0), s_w[n] = scale[n] * sx. */
+int mk_weight_row_amax(const void* w, int n_out, int n_in, float fold, float* amax, void* stream);
+int mk_weight_quantize(const void* w, int n_out, int n_in, float fold, const float* smooth, int fp8, float sx,
+                       void* codes, int ld_codes, float* scale_ws, float* s_w, void* stream);
+
 /* Weight repack (used by mk_model_create; exported for tests): out (N, K) = in (K, N)^T.
  * map 1: N == 2 * inter columns in the reference's gate/up layout with chunk ic, reordered into
  * 32-column gate/up interleave blocks. */

@@ -136,6 +136,22 @@ namespace {
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 }  // namespace
 
+int mk_weight_row_amax(const void* w, int n_out, int n_in, float fold, float* amax, void* stream) {
+  MK_REQUIRE(w && amax, "weight_row_amax: null pointer");
+  MK_REQUIRE(n_out >= 1 && n_in >= 1, "weight_row_amax: empty weight");
+  MK_TRY(mk::launch_weight_row_amax(static_cast<const uint16_t*>(w), n_out, n_in, fold, amax,
+                                    static_cast<hipStream_t>(stream)));
+}
+
+int mk_weight_quantize(const void* w, int n_out, int n_in, float fold, const float* smooth, int fp8, float sx,
+                       void* codes, int ld_codes, float* scale_ws, float* s_w, void* stream) {
+  MK_REQUIRE(w && codes && scale_ws && s_w, "weight_quantize: null pointer");
+  MK_REQUIRE(n_out >= 1 && n_in >= 1 && ld_codes >= n_out, "weight_quantize: bad shape or code row stride");
+  MK_TRY(mk::launch_weight_quantize(static_cast<const uint16_t*>(w), n_out, n_in, fold, smooth, fp8 != 0, sx,
+                                    static_cast<uint8_t*>(codes), ld_codes, scale_ws, s_w,
+                                    static_cast<hipStream_t>(stream)));
+}
+
 size_t mk_attn_scratch_bytes(int B, int S, int n_kv, int head_dim) {
   return mk::attn_scratch_bytes(B, S, n_kv, head_dim);
 }

@@ -31,6 +31,11 @@ constexpr int KT = 64;   // keys per K/V tile
 constexpr int G = 8;     // q heads per kv head == waves per workgroup
 constexpr int NT = 64 * G;
 
+// Workgroup (32-token block, job, sequence): jobs 0 .. n_kv - 1 RoPE the K of one kv head, jobs n_kv ..
+// 2 n_kv - 1 transpose the V of one.  Small independent workgroups (S / 32 x 2 n_kv per sequence) keep
+// enough loads in flight to stream K and V near HBM rate.
+constexpr int PT = 32;   // tokens per prep workgroup
+
 template <int HD>
 __global__ __launch_bounds__(256) void attn_prep_kernel(const uint16_t* __restrict__ qkv,
                                                         const uint16_t* __restrict__ cosr,
@@ -40,37 +45,43 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(const uint16_t* __restri
                                                         int n_kv, int* __restrict__ queue) {
   // the attention kernel's work queues start empty (vector atomics: no scalar-cache writes)
   if (blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && threadIdx.x <= n_kv) atomicExch(&queue[threadIdx.x], 0);
-  // 64 tokens of one kv head; 16-byte loads and stores throughout.  V goes through LDS for the
-  // transpose (row of 64 tokens + 8 pad elements: the column reads of 8 consecutive tokens spread
-  // over the banks).
-  constexpr int VR = 64 + 8;
-  __shared__ __attribute__((aligned(16))) uint16_t vs[HD][VR];
-  const int t0 = blockIdx.x * 64, kv = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
+  const int t0 = blockIdx.x * PT, job = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
   const int D = (n_q + 2 * n_kv) * HD;
   const uint16_t* base = qkv + ((size_t)b * S + t0) * D;
-  constexpr int H2 = HD / 2, NC = HD / 16;   // 16-byte chunks per half row
-  uint16_t* kdst = krope + (((size_t)b * n_kv + kv) * S + t0) * HD;
-  for (int idx = tid; idx < 64 * NC; idx += 256) {
-    const int t = idx / NC, c = idx % NC;
-    const uint16_t* kr = base + (size_t)t * D + (n_q + kv) * HD;
-    const size_t tb = (size_t)(t0 + t) * HD;
-    const u32x4 lo = *reinterpret_cast<const u32x4*>(kr + 8 * c);
-    const u32x4 hi = *reinterpret_cast<const u32x4*>(kr + H2 + 8 * c);
-    const u32x4 cl = *reinterpret_cast<const u32x4*>(cosr + tb + 8 * c);
-    const u32x4 ch = *reinterpret_cast<const u32x4*>(cosr + tb + H2 + 8 * c);
-    const u32x4 sl = *reinterpret_cast<const u32x4*>(sinr + tb + 8 * c);
-    const u32x4 sh = *reinterpret_cast<const u32x4*>(sinr + tb + H2 + 8 * c);
-    u32x4 olo, ohi;
+  if (job < n_kv) {
+    // K RoPE (rotate-half): 16-byte chunks c of both halves of a row, f32 products of the bf16 values,
+    // one rounding to bf16
+    const int kv = job;
+    constexpr int H2 = HD / 2, NC = HD / 16;   // 16-byte chunks per half row
+    uint16_t* kdst = krope + (((size_t)b * n_kv + kv) * S + t0) * HD;
+    for (int idx = tid; idx < PT * NC; idx += 256) {
+      const int t = idx / NC, c = idx % NC;
+      const uint16_t* kr = base + (size_t)t * D + (n_q + kv) * HD;
+      const size_t tb = (size_t)(t0 + t) * HD;
+      const u32x4 lo = *reinterpret_cast<const u32x4*>(kr + 8 * c);
+      const u32x4 hi = *reinterpret_cast<const u32x4*>(kr + H2 + 8 * c);
+      const u32x4 cl = *reinterpret_cast<const u32x4*>(cosr + tb + 8 * c);
+      const u32x4 ch = *reinterpret_cast<const u32x4*>(cosr + tb + H2 + 8 * c);
+      const u32x4 sl = *reinterpret_cast<const u32x4*>(sinr + tb + 8 * c);
+      const u32x4 sh = *reinterpret_cast<const u32x4*>(sinr + tb + H2 + 8 * c);
+      u32x4 olo, ohi;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float x1a = bf_lo(lo[e]), x1b = bf_hi(lo[e]), x2a = bf_lo(hi[e]), x2b = bf_hi(hi[e]);
-      olo[e] = pack_bf2(x1a * bf_lo(cl[e]) - x2a * bf_lo(sl[e]), x1b * bf_hi(cl[e]) - x2b * bf_hi(sl[e]));
-      ohi[e] = pack_bf2(x2a * bf_lo(ch[e]) + x1a * bf_lo(sh[e]), x2b * bf_hi(ch[e]) + x1b * bf_hi(sh[e]));
+      for (int e = 0; e < 4; ++e) {
+        const float x1a = bf_lo(lo[e]), x1b = bf_hi(lo[e]), x2a = bf_lo(hi[e]), x2b = bf_hi(hi[e]);
+        olo[e] = pack_bf2(x1a * bf_lo(cl[e]) - x2a * bf_lo(sl[e]), x1b * bf_hi(cl[e]) - x2b * bf_hi(sl[e]));
+        ohi[e] = pack_bf2(x2a * bf_lo(ch[e]) + x1a * bf_lo(sh[e]), x2b * bf_hi(ch[e]) + x1b * bf_hi(sh[e]));
+      }
+      *reinterpret_cast<u32x4*>(kdst + (size_t)t * HD + 8 * c) = olo;
+      *reinterpret_cast<u32x4*>(kdst + (size_t)t * HD + H2 + 8 * c) = ohi;
     }
-    *reinterpret_cast<u32x4*>(kdst + (size_t)t * HD + 8 * c) = olo;
-    *reinterpret_cast<u32x4*>(kdst + (size_t)t * HD + H2 + 8 * c) = ohi;
+    return;
   }
-  for (int idx = tid; idx < 64 * (HD / 8); idx += 256) {
+  // V transpose through LDS (row of 32 tokens + 8 pad elements: the column reads of 8 consecutive
+  // tokens spread over the banks)
+  const int kv = job - n_kv;
+  constexpr int VR = PT + 8;
+  __shared__ __attribute__((aligned(16))) uint16_t vs[HD][VR];
+  for (int idx = tid; idx < PT * (HD / 8); idx += 256) {
     const int t = idx / (HD / 8), c = idx % (HD / 8);
     const u32x4 v = *reinterpret_cast<const u32x4*>(base + (size_t)t * D + (n_q + n_kv + kv) * HD + 8 * c);
 #pragma unroll
@@ -85,8 +96,8 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(const uint16_t* __restri
   // lane's P^T column covers in the attention kernel, so that kernel copies V^T tiles into LDS as
   // plain 16-byte chunks
   uint16_t* vdst = vt + ((size_t)b * n_kv + kv) * HD * S + t0;
-  for (int idx = tid; idx < HD * 8; idx += 256) {
-    const int d = idx / 8, c = idx % 8;
+  for (int idx = tid; idx < HD * (PT / 8); idx += 256) {
+    const int d = idx / (PT / 8), c = idx % (PT / 8);
     const int k0 = 16 * (c >> 1) + 4 * (c & 1);
     const u32x2 lo = *reinterpret_cast<const u32x2*>(&vs[d][k0]);
     const u32x2 hi = *reinterpret_cast<const u32x2*>(&vs[d][k0 + 8]);
@@ -552,7 +563,7 @@ template <int HD>
 int launch_attn_hd(const AttnArgs& a, hipStream_t st, int stages) {
   int* queue = attn_queue(a);
   if (stages & 1) {
-    const dim3 pg(a.S / 64, a.n_kv, a.B);
+    const dim3 pg(a.S / PT, 2 * a.n_kv, a.B);
     hipLaunchKernelGGL(attn_prep_kernel<HD>, pg, dim3(256), 0, st, a.qkv, a.cos, a.sin, a.krope, a.vt,
                        a.S, a.n_q, a.n_kv, queue);
     MK_HIP_CHECK(hipGetLastError());

@@ -131,6 +131,15 @@ struct PackArgs {
 int launch_pack(const PackArgs& p, hipStream_t st);
 int launch_pack_scales(const float* in, float* out, int inter, int ic, hipStream_t st);
 
+// ------------------------------------------------------------------------------ weight preparation
+// HF weight w (n_out, n_in) bf16, W = w^T * fold (in, out) f32 (prep.hip):
+// aw[j] = max_n |W[j, n]|  (SmoothQuant's weight statistic)
+int launch_weight_row_amax(const uint16_t* w, int n_out, int n_in, float fold, float* aw, hipStream_t st);
+// per-output-channel 8-bit quantisation of W * smooth[j]: codes (in, out) at row stride ld, scale_ws[n] the
+// raw scale, s_w[n] = scale * sx
+int launch_weight_quantize(const uint16_t* w, int n_out, int n_in, float fold, const float* smooth, bool fp8, float sx,
+                           uint8_t* codes, int ld, float* scale_ws, float* s_w, hipStream_t st);
+
 // ------------------------------------------------------------------------------ measurement
 // MFMA-only throughput (random operands, 32x32 bf16 or int8) on every SIMD: the rate this board
 // sustains under its power limit, and the shader clock it ran at.

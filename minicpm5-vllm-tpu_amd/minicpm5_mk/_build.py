@@ -23,7 +23,7 @@ BUILD = os.path.join(PROJ, "_build")
 LIB = os.path.join(PKG, "libmk.so")
 ARCH = "gfx950"
 
-SOURCES = ["api.cpp", "model.cpp", "attn.hip", "gemm.hip", "norm.hip", "pack.hip", "peak.hip", "noalloc.hip"]
+SOURCES = ["api.cpp", "model.cpp", "attn.hip", "gemm.hip", "norm.hip", "pack.hip", "peak.hip", "noalloc.hip", "prep.hip"]
 # attention scores are finite or -inf, never NaN: without NaN semantics the row max needs no
 # canonicalising v_max per MFMA result
 EXTRA = {"attn.hip": ["-fno-honor-nans"]}

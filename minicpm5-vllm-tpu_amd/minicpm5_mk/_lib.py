@@ -63,6 +63,8 @@ SIGNATURES = {
     "mk_gemm": (_I, [_I, _I, _P, _I, _P, _I, _I, _I, _I, _P, _I, _P, _I, _P, _P, _P, _P]),
     "mk_lm_head": (_I, [_P, _P, _I, _I, _I, _P, _P]),
     "mk_pack_weight": (_I, [_P, _I, _P, _I, _I, _I, _I, _I, _I, _P]),
+    "mk_weight_row_amax": (_I, [_P, _I, _I, _F, _P, _P]),
+    "mk_weight_quantize": (_I, [_P, _I, _I, _F, _P, _I, _F, _P, _I, _P, _P, _P]),
     "mk_bench_attn": (_I, [_P, _P, _P, _P, _P, _SZ, _I, _I, _I, _I, _I, _F, _I, _P, ctypes.POINTER(_F)]),
     "mk_bench_gemm": (_I, [_I, _I, _P, _I, _P, _I, _I, _I, _I, _P, _I, _P, _I, _P, _P, _P, _I, _P,
                            ctypes.POINTER(_F)]),

@@ -116,8 +116,9 @@ class MkEngine:
         if state_dict is None:
             from .synth import random_hf_state_dict
             state_dict = random_hf_state_dict(cfg, seed=weight_seed)
-        w = prepare_mk_weights(state_dict, cfg.as_mk_cfg(), self.quant, max_model_len, cfg.bos_token_id, log=log)
         dev = self.device
+        w = prepare_mk_weights(state_dict, cfg.as_mk_cfg(), self.quant, max_model_len, cfg.bos_token_id, log=log,
+                               device=dev if dev.type == "cuda" else None)
         self.weights = {k: w[k].to(dev) for k in WEIGHT_ORDER}
         self.cos, self.sin = w["cos"].to(dev), w["sin"].to(dev)
         self.embed = state_dict["model.embed_tokens.weight"].to(BF16).to(dev)

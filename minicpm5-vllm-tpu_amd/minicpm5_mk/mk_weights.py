@@ -73,27 +73,30 @@ def interleave_gu(w_gu: torch.Tensor, s_gu: torch.Tensor, ic: int):
 
 
 # ---------------------------------------------------------------------------------------------- 1. layers
-def hf_layers(sd: Dict[str, torch.Tensor], cfg: dict, fold_qkv_gamma: bool, fold_gu_gamma: bool) -> list:
-    """Per-layer f32 dicts {w_qkv (H, D), w_o (q_dim, H), w_gu (H, 2, I), w_down (I, H), in_norm,
-    post_norm}.  Gammas are folded into the rows of bf16 linears only: a quantized linear keeps its
-    gamma in the activation factor, so outlier channels do not widen the weight's row range."""
+def hf_layer(sd: Dict[str, torch.Tensor], cfg: dict, i: int, fold_qkv_gamma: bool, fold_gu_gamma: bool) -> dict:
+    """Layer i as an f32 dict {w_qkv (H, D), w_o (q_dim, H), w_gu (H, 2, I), w_down (I, H), in_norm,
+    post_norm}, on the device of its HF tensors.  Gammas are folded into the rows of bf16 linears only:
+    a quantized linear keeps its gamma in the activation factor, so outlier channels do not widen the
+    weight's row range."""
     sm = 1.0 / math.sqrt(cfg["head_dim"])
-    out = []
-    for i in range(cfg["num_layers"]):
-        get = lambda n: sd[f"model.layers.{i}.{n}.weight"].to(F32)  # noqa: E731
-        g_in, g_post = get("input_layernorm"), get("post_attention_layernorm")
-        q, k, v = get("self_attn.q_proj").t() * sm, get("self_attn.k_proj").t(), get("self_attn.v_proj").t()
-        gate, up = get("mlp.gate_proj").t(), get("mlp.up_proj").t()
-        if fold_qkv_gamma:
-            q, k, v = (g_in[:, None] * t for t in (q, k, v))
-        if fold_gu_gamma:
-            gate, up = g_post[:, None] * gate, g_post[:, None] * up
-        out.append({"w_qkv": torch.cat([q, k, v], dim=1).contiguous(),
-                    "w_o": get("self_attn.o_proj").t().contiguous(),
-                    "w_gu": torch.stack([gate, up], dim=1).contiguous(),
-                    "w_down": get("mlp.down_proj").t().contiguous(),
-                    "in_norm": g_in, "post_norm": g_post})
-    return out
+    get = lambda n: sd[f"model.layers.{i}.{n}.weight"].to(F32)  # noqa: E731
+    g_in, g_post = get("input_layernorm"), get("post_attention_layernorm")
+    q, k, v = get("self_attn.q_proj").t() * sm, get("self_attn.k_proj").t(), get("self_attn.v_proj").t()
+    gate, up = get("mlp.gate_proj").t(), get("mlp.up_proj").t()
+    if fold_qkv_gamma:
+        q, k, v = (g_in[:, None] * t for t in (q, k, v))
+    if fold_gu_gamma:
+        gate, up = g_post[:, None] * gate, g_post[:, None] * up
+    return {"w_qkv": torch.cat([q, k, v], dim=1).contiguous(),
+            "w_o": get("self_attn.o_proj").t().contiguous(),
+            "w_gu": torch.stack([gate, up], dim=1).contiguous(),
+            "w_down": get("mlp.down_proj").t().contiguous(),
+            "in_norm": g_in, "post_norm": g_post}
+
+
+def hf_layers(sd: Dict[str, torch.Tensor], cfg: dict, fold_qkv_gamma: bool, fold_gu_gamma: bool) -> list:
+    """Every layer (hf_layer) in a list."""
+    return [hf_layer(sd, cfg, i, fold_qkv_gamma, fold_gu_gamma) for i in range(cfg["num_layers"])]
 
 
 # ---------------------------------------------------------------------------------------------- 2. calibration
@@ -177,12 +180,17 @@ def quantize_w(w: torch.Tensor, quant: str, sx: float):
     return codes, (scale.squeeze(0) * sx).to(F32)
 
 
-def smooth_factors(act_amax: torch.Tensor, w: torch.Tensor, alpha: float) -> torch.Tensor:
+def smooth_from_amax(act_amax: torch.Tensor, w_row_amax: torch.Tensor, alpha: float) -> torch.Tensor:
     """SmoothQuant factors per input channel j: amax_x[j]^alpha / amax_w[j]^(1 - alpha), both
     floored at 1e-5, clamped to [1e-4, 1e4] (mk_weights.py:229-238)."""
     ax = act_amax.to(F32).clamp(min=1e-5)
-    aw = w.reshape(w.shape[0], -1).abs().amax(dim=1).clamp(min=1e-5)
+    aw = w_row_amax.to(F32).clamp(min=1e-5)
     return (ax.pow(alpha) / aw.pow(1.0 - alpha)).clamp(1e-4, 1e4)
+
+
+def smooth_factors(act_amax: torch.Tensor, w: torch.Tensor, alpha: float) -> torch.Tensor:
+    """smooth_from_amax with the weight's per-input-row amax taken from W (in, ...)."""
+    return smooth_from_amax(act_amax, w.reshape(w.shape[0], -1).abs().amax(dim=1), alpha)
 
 
 @dataclass
@@ -192,27 +200,58 @@ class LinearQuantizer:
 
     A linear is dynamic (per-token activation scale at run time) for the d-bases and for the down
     projection of every base (mk_jax.py:422-423); otherwise its activation scale is the static one
-    from calibration, recalibrated on the smoothed activation when SmoothQuant is on."""
+    from calibration, recalibrated on the smoothed activation when SmoothQuant is on.  `plan` makes
+    the per-channel decisions from statistics only, so the GPU packer shares it."""
     base: str
     use_sq: bool
     alpha: float
     margin_override: float | None
 
-    def __call__(self, lin: str, w: torch.Tensor, gamma, static_scale: float, amax_all, amax_nob):
-        k_in = w.shape[0]
+    def plan(self, lin: str, k_in: int, gamma, static_scale: float, amax_all, amax_nob, w_row_amax):
+        """(smooth (in,) f32 or None, sx, a_x (in,) f32) from the calibration statistics and the
+        weight's per-input-row amax (w_row_amax: needed only with SmoothQuant)."""
         dynamic = self.base in ("int8d", "fp8d") or lin == "down"
-        smooth = torch.ones((k_in,), dtype=F32)
+        smooth = None
         if self.use_sq:
-            smooth = smooth_factors(amax_all, w, self.alpha)
-            w = w * smooth.view(-1, *([1] * (w.dim() - 1)))
+            smooth = smooth_from_amax(amax_all, w_row_amax, self.alpha)
             if not dynamic:
                 ax = amax_nob.to(F32) if self.base == "int8" else amax_all.to(F32).clamp(min=1e-5)
                 mg = self.margin_override if self.margin_override is not None else STATIC_MARGIN[self.base]
                 static_scale = max(float((ax / smooth).max()) * mg / QMAX[self.base], 1e-6)
         sx = 1.0 if dynamic else static_scale
+        sm = smooth if smooth is not None else torch.ones((k_in,), dtype=F32)
+        a_x = ((gamma if gamma is not None else torch.ones((k_in,), dtype=F32)) / (sm * sx)).to(F32)
+        return smooth, sx, a_x
+
+    def __call__(self, lin: str, w: torch.Tensor, gamma, static_scale: float, amax_all, amax_nob):
+        k_in = w.shape[0]
+        aw = w.reshape(k_in, -1).abs().amax(dim=1) if self.use_sq else None
+        smooth, sx, a_x = self.plan(lin, k_in, gamma, static_scale, amax_all, amax_nob, aw)
+        if smooth is not None:
+            w = w * smooth.view(-1, *([1] * (w.dim() - 1)))
         codes, s_w = quantize_w(w, self.base, sx)
-        a_x = ((gamma if gamma is not None else torch.ones((k_in,), dtype=F32)) / (smooth * sx)).to(F32)
         return codes, s_w, a_x
+
+
+def run_calibration(sd: Dict[str, torch.Tensor], cfg: dict, quant: str, layers) -> dict:
+    """The calibration forward with the reference's environment knobs (mk_weights.py:186-200) over
+    `layers` (any iterable of hf_layer dicts, consumed once in order): static scales, per-channel amax,
+    and the SmoothQuant settings."""
+    qm = parse_quant(quant)
+    base = quant.split("|")[0].split(":", 1)[0]
+    env = os.environ.get
+    s_cal, n_cal = int(env("MINICPM5_MK_CAL_SEQ", "128")), int(env("MINICPM5_MK_CAL_NSEQ", "4"))
+    m, md = env("MINICPM5_MK_CAL_MARGIN"), env("MINICPM5_MK_CAL_MARGIN_DOWN")
+    rc, rs = rope_tables(s_cal, cfg["head_dim"], cfg["rope_theta"])
+    scales, chan, chan_nob = calibrate(
+        layers, sd["model.embed_tokens.weight"].to("cpu", F32), rc.to(F32), rs.to(F32), cfg, base, n_seq=n_cal,
+        s_cal=s_cal, seed=int(env("MINICPM5_MK_CAL_SEED", "42")), margin=float(m) if m else None,
+        margin_down=float(md) if md else None, gamma_in_act={"qkv": qm["qkv"] != "bf16", "gu": qm["gu"] != "bf16"},
+        first_id=int(env("MINICPM5_MK_CAL_FIRST_ID", "1")))
+    return {"scales": scales, "chan": chan, "chan_nob": chan_nob,
+            "sq_stats": chan_nob if env("MINICPM5_MK_SQ_STATS", "all") == "nobos" else chan,
+            "alpha": float(env("MINICPM5_MK_SQ_ALPHA", "0.5")), "margin": float(m) if m else None,
+            "n_seq": n_cal, "s_cal": s_cal}
 
 
 # ---------------------------------------------------------------------------------------------- 4. assembly
@@ -226,12 +265,17 @@ def _last_layer_bf16(ld: dict, qm: dict) -> dict:
 
 @torch.no_grad()
 def prepare_mk_weights(sd: Dict[str, torch.Tensor], cfg: dict, quant: str, max_seq: int, bos_id: int = 0,
-                       log=print) -> Dict[str, torch.Tensor]:
-    """sd: HF-named CPU tensors; cfg: the _mk_cfg keys (num_layers, hidden, inter, n_q, n_kv, head_dim,
-    eps, rope_theta).  Returns CPU tensors in the megakernel layout (module docstring).  Environment
-    knobs of the reference: MINICPM5_MK_CAL_SEQ / _CAL_NSEQ / _CAL_SEED / _CAL_FIRST_ID /
+                       log=print, device=None) -> Dict[str, torch.Tensor]:
+    """sd: HF-named tensors; cfg: the _mk_cfg keys (num_layers, hidden, inter, n_q, n_kv, head_dim, eps,
+    rope_theta).  Returns tensors in the megakernel layout (module docstring): on the CPU, or, with a
+    CUDA `device`, prepared on that GPU by libmk's packer (minicpm5_mk.gpu_prep; bit-identical).
+    Environment knobs of the reference: MINICPM5_MK_CAL_SEQ / _CAL_NSEQ / _CAL_SEED / _CAL_FIRST_ID /
     _CAL_MARGIN / _CAL_MARGIN_DOWN, MINICPM5_MK_SQ_ALPHA, MINICPM5_MK_SQ_STATS (all | nobos)."""
     del bos_id  # signature parity: the calibration's first id is MINICPM5_MK_CAL_FIRST_ID
+    if device is not None and torch.device(device).type == "cuda":
+        from .gpu_prep import prepare_on_gpu
+
+        return prepare_on_gpu(sd, cfg, quant, max_seq, log=log, device=device)
     t0 = time.perf_counter()
     qm = parse_quant(quant)
     flags = quant_flags(quant)
@@ -248,17 +292,9 @@ def prepare_mk_weights(sd: Dict[str, torch.Tensor], cfg: dict, quant: str, max_s
         log(f"[mk] bf16 weights prepared (L-1={len(scan)} + last) in {time.perf_counter() - t0:.1f}s")
         return out
 
-    env = os.environ.get
-    s_cal, n_cal = int(env("MINICPM5_MK_CAL_SEQ", "128")), int(env("MINICPM5_MK_CAL_NSEQ", "4"))
-    m, md = env("MINICPM5_MK_CAL_MARGIN"), env("MINICPM5_MK_CAL_MARGIN_DOWN")
-    rc, rs = rope_tables(s_cal, cfg["head_dim"], cfg["rope_theta"])
-    scales, chan, chan_nob = calibrate(
-        layers, sd["model.embed_tokens.weight"].to(F32), rc.to(F32), rs.to(F32), cfg, base, n_seq=n_cal, s_cal=s_cal,
-        seed=int(env("MINICPM5_MK_CAL_SEED", "42")), margin=float(m) if m else None,
-        margin_down=float(md) if md else None, gamma_in_act={"qkv": qm["qkv"] != "bf16", "gu": qm["gu"] != "bf16"},
-        first_id=int(env("MINICPM5_MK_CAL_FIRST_ID", "1")))
-    alpha = float(env("MINICPM5_MK_SQ_ALPHA", "0.5"))
-    sq_stats = chan_nob if env("MINICPM5_MK_SQ_STATS", "all") == "nobos" else chan
+    cal = run_calibration(sd, cfg, quant, layers)
+    scales, chan_nob, sq_stats = cal["scales"], cal["chan_nob"], cal["sq_stats"]
+    alpha, m, n_cal, s_cal = cal["alpha"], cal["margin"], cal["n_seq"], cal["s_cal"]
     stacks = {f"{p}_{lin}": [] for p in ("w", "s", "a") for lin in LINEARS}
     dummy = torch.zeros((1,), dtype=F32)
     for li, ld in enumerate(scan):
@@ -267,7 +303,7 @@ def prepare_mk_weights(sd: Dict[str, torch.Tensor], cfg: dict, quant: str, max_s
             if qm[lin] == "bf16":
                 parts = (w.to(BF16), dummy, dummy)
             else:
-                qz = LinearQuantizer(qm[lin], "sq" in flags, alpha, float(m) if m else None)
+                qz = LinearQuantizer(qm[lin], "sq" in flags, alpha, m)
                 gamma = ld["in_norm"] if lin == "qkv" else ld["post_norm"] if lin == "gu" else None
                 parts = qz(lin, w, gamma, scales[li][lin], sq_stats[li][lin], chan_nob[li][lin])
             for p, t in zip(("w", "s", "a"), parts):

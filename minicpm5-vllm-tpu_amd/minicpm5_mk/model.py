@@ -114,8 +114,9 @@ class MiniCPM5MegakernelForCausalLM(LlamaForCausalLM):
         t0 = time.perf_counter()
         c = self._mk_cfg
         quant, _ = resolve_quant_pair(os.environ.get("MINICPM5_MK_QUANT", "auto"), c.num_layers, 1, c.hidden, c.inter)
-        w = prepare_mk_weights(stash, c.as_mk_cfg(), quant, self._mk_max_seq, c.bos_token_id, log=logger.info)
         dev = self.lm_head.weight.device
+        w = prepare_mk_weights(stash, c.as_mk_cfg(), quant, self._mk_max_seq, c.bos_token_id, log=logger.info,
+                               device=dev if dev.type == "cuda" else None)
         emb = self.model.embed_tokens.weight
         embed = emb.data if emb.dtype == torch.bfloat16 else stash["model.embed_tokens.weight"].to(torch.bfloat16).to(dev)
         self._mk_keep = {k: w[k].to(dev) for k in WEIGHT_ORDER}
