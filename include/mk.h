@@ -118,6 +118,13 @@ int mk_forward(mk_model* m, const int32_t* input_ids, int bs, int seq, void* hid
 /* 1 (default) replays captured hipGraphs, 0 launches kernels eagerly on every call. */
 int mk_set_graph_mode(mk_model* m, int enable);
 
+/* Large batches run in chunks of sequences, one after another in one workspace of chunk size (the
+ * reference's microbatching, mk_jax.py:572-605): by default as many sequences as keep every GEMM operand
+ * under 4 GiB (e.g. 21 x 8192 tokens for MiniCPM5-2B with an int8 down projection, 42 with bf16);
+ * seqs > 0 caps the chunk further (smaller workspace), 0 restores the default.  Results do not depend
+ * on the chunking.  mk_workspace_bytes follows the setting. */
+int mk_set_max_chunk(mk_model* m, int seqs);
+
 /* Kernel categories of mk_forward_timed. */
 enum {
   MK_KERNEL_EMBED = 0,      /* embedding gather */

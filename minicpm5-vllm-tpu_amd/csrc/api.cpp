@@ -106,7 +106,7 @@ int mk_workspace_bytes(const mk_model* m, int bs, int seq, size_t* bytes) {
   int rc = mk::validate_run(m->impl->cfg, bs, seq);
   if (rc) return rc;
   mk::WorkLayout W{};
-  mk::workspace_layout(*m->impl, bs, seq, &W);
+  mk::workspace_layout(*m->impl, mk::chunk_seqs(*m->impl, bs, seq), seq, &W);
   *bytes = W.total;
   return MK_OK;
 }
@@ -128,6 +128,17 @@ int mk_forward_timed(mk_model* m, const int32_t* input_ids, int bs, int seq, voi
 int mk_set_graph_mode(mk_model* m, int enable) {
   MK_REQUIRE(m != nullptr, "set_graph_mode: null model");
   m->impl->use_graph = enable != 0;
+  return MK_OK;
+}
+
+int mk_set_max_chunk(mk_model* m, int seqs) {
+  MK_REQUIRE(m != nullptr, "set_max_chunk: null model");
+  MK_REQUIRE(seqs >= 0, "set_max_chunk: seqs must be >= 0");
+  if (m->impl->max_chunk != seqs) {   // captured graphs hold the old chunking
+    for (auto& g : m->impl->graphs) hipGraphExecDestroy(g.exec);
+    m->impl->graphs.clear();
+  }
+  m->impl->max_chunk = seqs;
   return MK_OK;
 }
 

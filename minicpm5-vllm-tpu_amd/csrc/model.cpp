@@ -160,6 +160,19 @@ int packed_layout(const mk_config* c, const QuantPlan& q, PackedLayout* L) {
   return MK_OK;
 }
 
+int chunk_seqs(const Model& m, int bs, int S) {
+  const mk_config& c = m.cfg;
+  const size_t H = c.hidden, I = c.inter;
+  const size_t qd = (size_t)c.n_q * c.head_dim, D = qd + 2 * (size_t)c.n_kv * c.head_dim;
+  const bool d8 = m.q.fmlp && m.q.i8[3];
+  // the widest token row of any activation buffer a GEMM reads or writes
+  const size_t row = std::max({H * 2, std::max({H, qd, I}), D * 2, qd * 2, I * (d8 ? 4 : 2)});
+  const size_t lim = ((size_t)1 << 32) - 1;
+  int cb = (int)std::min<size_t>((size_t)bs, std::max<size_t>(1, lim / (row * (size_t)S)));
+  if (m.max_chunk > 0) cb = std::min(cb, m.max_chunk);
+  return cb;
+}
+
 int workspace_layout(const Model& m, int B, int S, WorkLayout* W) {
   const mk_config& c = m.cfg;
   const size_t T = (size_t)B * S, H = c.hidden, I = c.inter;
@@ -309,6 +322,7 @@ struct Fwd {
   char* ws;
   WorkLayout W;
   KernelTimer* tm = nullptr;
+  bool pad = true;   // zero the output rows B .. max(8, B) - 1 (off for the chunks of a larger batch)
 };
 
 int launch_forward(const Fwd& f, hipStream_t st) {
@@ -625,7 +639,7 @@ int launch_forward(const Fwd& f, hipStream_t st) {
   }
   // ---- final norm into the (max(8, B), H) output, pad rows zero (mk_jax.py:569, :608-612)
   const int rows_out = std::max(8, B);
-  if (rows_out > B) MK_RUN(launch_zero(f.hidden + (size_t)B * H, (size_t)(rows_out - B) * H * 2, st));
+  if (f.pad && rows_out > B) MK_RUN(launch_zero(f.hidden + (size_t)B * H, (size_t)(rows_out - B) * H * 2, st));
   MK_RUN(launch_rmsnorm_bf16(xl, H, static_cast<const uint16_t*>(m.w.final_norm), f.hidden, H, B, H, c.eps, st));
   kind = MK_KERNEL_LM_HEAD;
   if (f.logits) {
@@ -650,6 +664,24 @@ int launch_forward(const Fwd& f, hipStream_t st) {
   return MK_OK;
 }
 
+// The whole (bs, seq) forward: one launch sequence, or chunks of chunk_seqs() sequences each writing
+// their rows of hidden / logits, then the zero padding rows.
+int launch_batches(const Model& m, const int32_t* ids, int bs, int seq, uint16_t* hidden, float* logits, char* ws,
+                   const WorkLayout& W, KernelTimer* tm, hipStream_t st) {
+  const int cb = chunk_seqs(m, bs, seq), H = m.cfg.hidden, V = m.cfg.vocab;
+  if (cb >= bs) return launch_forward(Fwd{m, ids, bs, seq, hidden, logits, ws, W, tm}, st);
+  for (int b0 = 0; b0 < bs; b0 += cb) {
+    Fwd f{m, ids + (size_t)b0 * seq, std::min(cb, bs - b0), seq, hidden + (size_t)b0 * H,
+          logits ? logits + (size_t)b0 * V : nullptr, ws, W, tm};
+    f.pad = false;
+    const int rc = launch_forward(f, st);
+    if (rc) return rc;
+  }
+  const int rows_out = std::max(8, bs);
+  if (rows_out > bs) return launch_zero(hidden + (size_t)bs * H, (size_t)(rows_out - bs) * H * 2, st);
+  return MK_OK;
+}
+
 }  // namespace
 
 int validate_run(const mk_config& c, int bs, int seq) {
@@ -669,11 +701,10 @@ int model_forward_timed(Model* m, const int32_t* ids, int bs, int seq, void* hid
   MK_REQUIRE(ids && hidden && ws, "forward_timed: null ids / output / workspace");
   MK_REQUIRE(!logits || m->w.lm_head, "forward_timed: logits requested but the model has no lm_head");
   WorkLayout W{};
-  workspace_layout(*m, bs, seq, &W);
+  workspace_layout(*m, chunk_seqs(*m, bs, seq), seq, &W);
   MK_REQUIRE(ws_bytes >= W.total, "forward_timed: workspace too small");
   KernelTimer tm;
-  Fwd f{*m, ids, bs, seq, static_cast<uint16_t*>(hidden), logits, static_cast<char*>(ws), W, &tm};
-  rc = launch_forward(f, st);
+  rc = launch_batches(*m, ids, bs, seq, static_cast<uint16_t*>(hidden), logits, static_cast<char*>(ws), W, &tm, st);
   if (rc) return rc;
   MK_HIP_CHECK(hipStreamSynchronize(st));
   for (int k = 0; k < MK_KERNEL_KINDS; ++k) {
@@ -697,13 +728,14 @@ int model_forward(Model* m, const int32_t* ids, int bs, int seq, void* hidden, f
   MK_REQUIRE(ids && hidden && ws, "forward: null ids / output / workspace");
   MK_REQUIRE(!logits || m->w.lm_head, "forward: logits requested but the model has no lm_head");
   WorkLayout W{};
-  workspace_layout(*m, bs, seq, &W);
+  workspace_layout(*m, chunk_seqs(*m, bs, seq), seq, &W);
   if (ws_bytes < W.total) {
     set_error("forward: workspace too small (" + std::to_string(ws_bytes) + " < " + std::to_string(W.total) + ")");
     return MK_ENOMEM;
   }
-  Fwd f{*m, ids, bs, seq, static_cast<uint16_t*>(hidden), logits, static_cast<char*>(ws), W};
-  if (!m->use_graph) return launch_forward(f, st);
+  uint16_t* hid = static_cast<uint16_t*>(hidden);
+  char* wsp = static_cast<char*>(ws);
+  if (!m->use_graph) return launch_batches(*m, ids, bs, seq, hid, logits, wsp, W, nullptr, st);
 
   GraphKey key{bs, seq, ids, hidden, logits, ws};
   for (auto& g : m->graphs) {
@@ -713,7 +745,7 @@ int model_forward(Model* m, const int32_t* ids, int bs, int seq, void* hidden, f
     }
   }
   MK_HIP_CHECK(hipStreamBeginCapture(m->cap_stream, hipStreamCaptureModeThreadLocal));
-  rc = launch_forward(f, m->cap_stream);
+  rc = launch_batches(*m, ids, bs, seq, hid, logits, wsp, W, nullptr, m->cap_stream);
   hipGraph_t graph = nullptr;
   hipError_t e = hipStreamEndCapture(m->cap_stream, &graph);
   if (rc) {

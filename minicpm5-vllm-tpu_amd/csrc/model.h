@@ -52,6 +52,7 @@ struct Model {
   PackedLayout P{};
   char* packed = nullptr;
   bool use_graph = true;
+  int max_chunk = 0;   // caller's cap on sequences per chunk (0: only the 4 GiB operand limit)
   hipStream_t cap_stream = nullptr;
   std::vector<CachedGraph> graphs;
   ~Model();
@@ -62,6 +63,10 @@ int validate_config(const mk_config* c);
 int validate_run(const mk_config& c, int bs, int seq);
 int packed_layout(const mk_config* c, const QuantPlan& q, PackedLayout* L);
 int workspace_layout(const Model& m, int B, int S, WorkLayout* W);
+// Sequences per chunk of a (bs, S) forward: every GEMM operand of a chunk spans < 4 GiB (32-bit
+// operand offsets), at most m.max_chunk when set.  The forward runs the chunks one after another with
+// one workspace of chunk size (the reference's microbatching, mk_jax.py:572-605).
+int chunk_seqs(const Model& m, int bs, int S);
 int model_create(const mk_config* cfg, const char* quant, const mk_weights* w, void* packed, size_t packed_bytes,
                  hipStream_t st, Model** out);
 // Eager forward with an event pair around every launch: per-kind kernel time (ms) and launch counts,

@@ -121,6 +121,12 @@ class MkModel:
     def set_graph_mode(self, enable: bool) -> None:
         check(load().mk_set_graph_mode(self._h, int(enable)), "mk_set_graph_mode")
 
+    def set_max_chunk(self, seqs: int) -> None:
+        """Cap the sequences per chunk of a large batch (0 = the default, include/mk.h); drops the cached
+        per-shape buffers, whose workspace size depends on it."""
+        check(load().mk_set_max_chunk(self._h, int(seqs)), "mk_set_max_chunk")
+        self._bufs.clear()
+
     def workspace_bytes(self, bs: int, seq: int) -> int:
         n = ctypes.c_size_t()
         check(load().mk_workspace_bytes(self._h, bs, seq, ctypes.byref(n)), "mk_workspace_bytes")

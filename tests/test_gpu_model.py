@@ -255,8 +255,10 @@ def test_two_layer_full_size_vs_emulator(name):
 TWO_LAYER = {"1b": (0.07, 0.012), "1b-hd96": (0.08, 0.012), "2b": (0.15, 0.023)}
 
 
-# (preset, batch sizes): BASELINE configs 4 (1B-hd96, B = 4..32) and 5 (2B), plus the reference's 1B.
-BATCH = [("1b-hd96", 4), ("1b-hd96", 8), ("1b-hd96", 16), ("1b-hd96", 32), ("1b", 4), ("1b", 32), ("2b", 4), ("2b", 32)]
+# (preset, batch sizes): BASELINE configs 4 (1B-hd96, B = 4..32) and 5 (2B), plus the reference's 1B; 2B at
+# B = 48 runs in two chunks (42 + 6 sequences: the (T, I) bf16 activation of 48 x 8192 tokens exceeds 4 GiB).
+BATCH = [("1b-hd96", 4), ("1b-hd96", 8), ("1b-hd96", 16), ("1b-hd96", 32), ("1b", 4), ("1b", 32), ("2b", 4), ("2b", 32),
+         ("2b", 48)]
 
 
 @pytest.mark.parametrize("name,B", BATCH)
@@ -321,6 +323,34 @@ def test_batch_invariance_and_graph_replay():
     eager = m.forward(ids.reshape(-1), 4, 1024, logits=True)[1]
     for o in outs:
         assert torch.equal(o, eager)
+    m.close()
+
+
+@pytest.mark.parametrize("B,chunk", [(5, 2), (3, 2), (9, 4)])
+def test_chunked_batches_equal_one_launch(B, chunk):
+    """A batch run in chunks of sequences (mk_set_max_chunk; by default only past the 4 GiB operand limit)
+    gives the same rows and logits bitwise, padding rows zero, in graph and eager mode."""
+    from minicpm5_mk.config import preset
+    from minicpm5_mk.synth import random_hf_state_dict, random_token_ids
+
+    dev = _dev()
+    cfg = preset("tiny")
+    sd = random_hf_state_dict(cfg)
+    m, _ = _build(cfg, "int8d:qkv+gu+o|sq|lastbf16|fqkv|fmlp", sd, 1024, dev)
+    ids = random_token_ids(B, 512, seed=B).to(dev).reshape(-1)
+    h_all, l_all = m.forward(ids, B, 512, logits=True)
+    ws_all = m.workspace_bytes(B, 512)
+    m.set_max_chunk(chunk)
+    assert m.workspace_bytes(B, 512) < ws_all
+    for graph in (True, False):
+        m.set_graph_mode(graph)
+        h_c, l_c = m.forward(ids, B, 512, logits=True)
+        assert torch.equal(h_c, h_all) and torch.equal(l_c, l_all)
+        assert torch.equal(h_c[B:], torch.zeros_like(h_c[B:]))
+    t = m.forward_timed(ids, B, 512, logits=True)
+    assert t["attn"][1] == (cfg.num_layers - 1) * ((B + chunk - 1) // chunk)
+    m.set_max_chunk(0)
+    assert m.workspace_bytes(B, 512) == ws_all
     m.close()
 
 
