@@ -41,7 +41,8 @@ PEAK = {"bf16": 2516.6, "int8": 5033.2, "fp8": 5033.2, "hbm": 8000.0}   # MI355X
 METRIC = "prefill tokens/sec at (B,8192) B=1..32, 1B and 2B arch; p50 ms at (1,8192)"
 # HBM bytes per attn_fwd_kernel launch measured by rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (scaled by a
 # 256 MiB copy's counters) for the default workload; (arch, B, S, quant) -> (bytes, source file)
-ATTN_TRAFFIC = {("1b", 1, 8192, "auto"): (77.1e6 + 33.6e6, "profiles/mfma_util_hbm_1b_b1_s8192.txt")}
+ATTN_TRAFFIC = {("1b", 1, 8192, "auto"): (77.0e6 + 33.6e6, "profiles/mfma_util_hbm_1b_b1_s8192.txt"),
+                ("2b", 1, 8192, "auto"): (77.1e6 + 33.6e6, "profiles/mfma_util_hbm_2b_b1_s8192.txt")}
 DEFAULT_SWEEP = "1b:4,8,16,32;2b:1,4,8,16,32;1b-hd96:1"
 
 
