@@ -115,6 +115,16 @@ int mk_workspace_bytes(const mk_model* m, int bs, int seq, size_t* bytes);
 int mk_forward(mk_model* m, const int32_t* input_ids, int bs, int seq, void* hidden_out, float* logits_out,
                void* workspace, size_t workspace_bytes, void* stream);
 
+/* Per-shape precompile (MINICPM5_MK_PRECOMPILE, model.py:690-698): captures and instantiates the
+ * hipGraph mk_forward replays for (bs, seq) and exactly these buffers, without running it, so the first
+ * mk_forward of that shape does not pay the capture.  Same arguments and checks as mk_forward; nothing is
+ * launched and the buffers' contents are not read.  No-op when the graph is cached. */
+int mk_precompile(mk_model* m, const int32_t* input_ids, int bs, int seq, void* hidden_out, float* logits_out,
+                  void* workspace, size_t workspace_bytes);
+
+/* Number of hipGraphs the model holds (at most 16: the least recently captured is dropped first). */
+int mk_graph_count(const mk_model* m, int* n);
+
 /* 1 (default) replays captured hipGraphs, 0 launches kernels eagerly on every call. */
 int mk_set_graph_mode(mk_model* m, int enable);
 

@@ -125,6 +125,18 @@ int mk_forward_timed(mk_model* m, const int32_t* input_ids, int bs, int seq, voi
                                  static_cast<hipStream_t>(stream), ms, launches));
 }
 
+int mk_precompile(mk_model* m, const int32_t* input_ids, int bs, int seq, void* hidden_out, float* logits_out,
+                  void* workspace, size_t workspace_bytes) {
+  MK_REQUIRE(m != nullptr, "precompile: null model");
+  MK_TRY(mk::model_precompile(m->impl, input_ids, bs, seq, hidden_out, logits_out, workspace, workspace_bytes));
+}
+
+int mk_graph_count(const mk_model* m, int* n) {
+  MK_REQUIRE(m != nullptr && n != nullptr, "graph_count: null argument");
+  *n = (int)m->impl->graphs.size();
+  return MK_OK;
+}
+
 int mk_set_graph_mode(mk_model* m, int enable) {
   MK_REQUIRE(m != nullptr, "set_graph_mode: null model");
   m->impl->use_graph = enable != 0;

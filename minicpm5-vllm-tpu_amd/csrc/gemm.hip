@@ -65,6 +65,8 @@ using CfgX = GemmCfg<256, 256, 2, 4, 4, 1, 1>;
 // 256x192 block, 8 waves of 64x96 (two per SIMD), one workgroup per CU: N = 1536 in 8 column tiles, so
 // M = 8192 fills exactly 256 CUs
 using CfgN = GemmCfg<256, 192, 4, 2, 4, 1, 1>;
+// the same with a 5-stage ring (four stages of loads in flight)
+using CfgN5 = GemmCfg<256, 192, 4, 2, 5, 1, 1>;
 
 template <GemmIn IN>
 struct Mma;
@@ -665,12 +667,12 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(GemmArgs g, int spli
 // 256x128 workgroups.
 int choose_cfg(const GemmArgs& g) {
   const bool silu = g.epi == Epi::DQ_SILU || g.epi == Epi::DQ_SILU_F32A || g.epi == Epi::SILU_BF16;
-  if (g.cfg >= 1 && g.cfg <= 5 && !(silu && g.cfg == 5)) return g.cfg;
+  if (g.cfg >= 1 && g.cfg <= 6 && !(silu && g.cfg >= 5)) return g.cfg;
   static const int forced = [] {
-    const char* e = std::getenv("MK_GEMM_CFG");   // tuning override: 1 .. 5
+    const char* e = std::getenv("MK_GEMM_CFG");   // tuning override: 1 .. 6
     return e ? std::atoi(e) : 0;
   }();
-  if (forced >= 1 && forced <= 5 && !(silu && forced == 5)) return forced;
+  if (forced >= 1 && forced <= 6 && !(silu && forced >= 5)) return forced;
   struct Opt { int id, bm, bn; double eff; };
   const Opt opts[5] = {{4, 256, 256, silu ? 1.05 : 1.25}, {2, 256, 128, 1.0}, {1, 256, 256, 0.9},
                        {3, 128, 128, 0.85}, {5, 256, 192, 1.15}};
@@ -706,16 +708,16 @@ void launch_c(const GemmArgs& g0, hipStream_t st) {
 
 template <GemmIn IN, Epi EPI>
 void launch_t(const GemmArgs& g, hipStream_t st) {
+  constexpr bool silu = EPI == Epi::DQ_SILU || EPI == Epi::DQ_SILU_F32A || EPI == Epi::SILU_BF16;
   switch (choose_cfg(g)) {
     case 1: launch_c<CfgL, IN, EPI>(g, st); break;
     case 3: launch_c<CfgS, IN, EPI>(g, st); break;
     case 4: launch_c<CfgX, IN, EPI>(g, st); break;
     case 5:
-      if constexpr (EPI != Epi::DQ_SILU && EPI != Epi::DQ_SILU_F32A && EPI != Epi::SILU_BF16) {
-        launch_c<CfgN, IN, EPI>(g, st);
-        break;
-      }
-      launch_c<CfgM, IN, EPI>(g, st);
+      if constexpr (!silu) launch_c<CfgN, IN, EPI>(g, st);
+      break;
+    case 6:
+      if constexpr (!silu) launch_c<CfgN5, IN, EPI>(g, st);
       break;
     default: launch_c<CfgM, IN, EPI>(g, st); break;
   }

@@ -720,32 +720,38 @@ int model_forward_timed(Model* m, const int32_t* ids, int bs, int seq, void* hid
   return MK_OK;
 }
 
-int model_forward(Model* m, const int32_t* ids, int bs, int seq, void* hidden, float* logits, void* ws,
-                  size_t ws_bytes, hipStream_t st) {
-  MK_REQUIRE(m != nullptr, "forward: null model");
+namespace {
+
+int check_run(const Model* m, const int32_t* ids, int bs, int seq, const void* hidden, const float* logits,
+              const void* ws, size_t ws_bytes, WorkLayout* W, const char* who) {
+  MK_REQUIRE(m != nullptr, std::string(who) + ": null model");
   int rc = validate_run(m->cfg, bs, seq);
   if (rc) return rc;
-  MK_REQUIRE(ids && hidden && ws, "forward: null ids / output / workspace");
-  MK_REQUIRE(!logits || m->w.lm_head, "forward: logits requested but the model has no lm_head");
-  WorkLayout W{};
-  workspace_layout(*m, chunk_seqs(*m, bs, seq), seq, &W);
-  if (ws_bytes < W.total) {
-    set_error("forward: workspace too small (" + std::to_string(ws_bytes) + " < " + std::to_string(W.total) + ")");
+  MK_REQUIRE(ids && hidden && ws, std::string(who) + ": null ids / output / workspace");
+  MK_REQUIRE(!logits || m->w.lm_head, std::string(who) + ": logits requested but the model has no lm_head");
+  workspace_layout(*m, chunk_seqs(*m, bs, seq), seq, W);
+  if (ws_bytes < W->total) {
+    set_error(std::string(who) + ": workspace too small (" + std::to_string(ws_bytes) + " < " +
+              std::to_string(W->total) + ")");
     return MK_ENOMEM;
   }
-  uint16_t* hid = static_cast<uint16_t*>(hidden);
-  char* wsp = static_cast<char*>(ws);
-  if (!m->use_graph) return launch_batches(*m, ids, bs, seq, hid, logits, wsp, W, nullptr, st);
+  return MK_OK;
+}
 
-  GraphKey key{bs, seq, ids, hidden, logits, ws};
+// The cached graph of `key`, captured (launches recorded on the model's private capture stream, nothing
+// executed) and instantiated on first use.  The cache keeps the kMaxGraphs most recently captured shapes.
+int graph_for(Model* m, const GraphKey& key, const WorkLayout& W, hipGraphExec_t* out) {
   for (auto& g : m->graphs) {
     if (g.key == key) {
-      MK_HIP_CHECK(hipGraphLaunch(g.exec, st));
+      *out = g.exec;
       return MK_OK;
     }
   }
   MK_HIP_CHECK(hipStreamBeginCapture(m->cap_stream, hipStreamCaptureModeThreadLocal));
-  rc = launch_batches(*m, ids, bs, seq, hid, logits, wsp, W, nullptr, m->cap_stream);
+  int rc = launch_batches(*m, static_cast<const int32_t*>(key.ids), key.bs, key.seq,
+                          static_cast<uint16_t*>(const_cast<void*>(key.hidden)),
+                          static_cast<float*>(const_cast<void*>(key.logits)),
+                          static_cast<char*>(const_cast<void*>(key.ws)), W, nullptr, m->cap_stream);
   hipGraph_t graph = nullptr;
   hipError_t e = hipStreamEndCapture(m->cap_stream, &graph);
   if (rc) {
@@ -768,8 +774,34 @@ int model_forward(Model* m, const int32_t* ids, int bs, int seq, void* hidden, f
     m->graphs.erase(m->graphs.begin());
   }
   m->graphs.push_back({key, exec});
+  *out = exec;
+  return MK_OK;
+}
+
+}  // namespace
+
+int model_forward(Model* m, const int32_t* ids, int bs, int seq, void* hidden, float* logits, void* ws,
+                  size_t ws_bytes, hipStream_t st) {
+  WorkLayout W{};
+  int rc = check_run(m, ids, bs, seq, hidden, logits, ws, ws_bytes, &W, "forward");
+  if (rc) return rc;
+  if (!m->use_graph)
+    return launch_batches(*m, ids, bs, seq, static_cast<uint16_t*>(hidden), logits, static_cast<char*>(ws), W,
+                          nullptr, st);
+  hipGraphExec_t exec = nullptr;
+  rc = graph_for(m, GraphKey{bs, seq, ids, hidden, logits, ws}, W, &exec);
+  if (rc) return rc;
   MK_HIP_CHECK(hipGraphLaunch(exec, st));
   return MK_OK;
+}
+
+int model_precompile(Model* m, const int32_t* ids, int bs, int seq, void* hidden, float* logits, void* ws,
+                     size_t ws_bytes) {
+  WorkLayout W{};
+  int rc = check_run(m, ids, bs, seq, hidden, logits, ws, ws_bytes, &W, "precompile");
+  if (rc) return rc;
+  hipGraphExec_t exec = nullptr;
+  return graph_for(m, GraphKey{bs, seq, ids, hidden, logits, ws}, W, &exec);
 }
 
 }  // namespace mk

@@ -75,5 +75,8 @@ int model_forward_timed(Model* m, const int32_t* ids, int bs, int seq, void* hid
                         size_t ws_bytes, hipStream_t st, float* ms, int* launches);
 int model_forward(Model* m, const int32_t* ids, int bs, int seq, void* hidden, float* logits, void* ws,
                   size_t ws_bytes, hipStream_t st);
+// Captures and instantiates the hipGraph of (bs, seq, buffers) without running it (no-op when cached).
+int model_precompile(Model* m, const int32_t* ids, int bs, int seq, void* hidden, float* logits, void* ws,
+                     size_t ws_bytes);
 
 }  // namespace mk

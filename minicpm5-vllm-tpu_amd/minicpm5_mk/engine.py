@@ -27,7 +27,7 @@ from .config import MkConfig, preset
 from .dispatch import StepView, eligible_step, mk_seq_ok
 from .mk_weights import prepare_mk_weights
 from .quant import resolve_quant_pair
-from .runtime import WEIGHT_ORDER, MkModel
+from .runtime import WEIGHT_ORDER, MkModel, parse_precompile
 
 BF16 = torch.bfloat16
 
@@ -101,7 +101,7 @@ def eligible_batch(prompts, sps, max_seq: int, require_mt1: bool = True):
 
 class MkEngine:
     def __init__(self, model="1b", quant: str = "auto", state_dict: dict | None = None, weight_seed: int = 0,
-                 max_model_len: int = 8256, device: str = "cuda:0", log=print):
+                 max_model_len: int = 8256, device: str = "cuda:0", log=print, precompile: str | None = None):
         t0 = time.perf_counter()
         if isinstance(model, str) and os.path.isdir(model):   # local HF checkpoint directory
             from .checkpoint import load_local_checkpoint
@@ -131,6 +131,13 @@ class MkEngine:
         self.status = {"arch": "MiniCPM5MegakernelForCausalLM", "quant": self.quant, "config": cfg.as_mk_cfg(),
                        "shapes": {}}
         log(f"[mk] engine ready ({cfg.name}, quant={self.quant}) in {time.perf_counter() - t0:.1f}s")
+        # per-shape graphs at load time (MINICPM5_MK_PRECOMPILE="1x8192,4x8192", model.py:690-698)
+        pre = os.environ.get("MINICPM5_MK_PRECOMPILE", "") if precompile is None else precompile
+        shapes = parse_precompile(pre)
+        for _, s in shapes:
+            if not mk_seq_ok(s, self.max_seq):
+                raise NotEligible("seq", f"precompile seq {s} not served")
+        self.model.precompile(shapes, logits=True, log=log)
 
     # ------------------------------------------------------------------ scoring
     @torch.no_grad()

@@ -19,7 +19,7 @@ selection reads.
 
 Requires vLLM (imported at module import, like the reference).  Environment knobs kept from the
 reference (model.py:23-32): MINICPM5_MK_ENABLE, MINICPM5_MK_QUANT, MINICPM5_MK_ATTN,
-MINICPM5_MK_REQUIRE_MAX_TOKENS_1, MINICPM5_MK_FREE_STOCK, MINICPM5_MK_STATUS_DIR; and
+MINICPM5_MK_REQUIRE_MAX_TOKENS_1, MINICPM5_MK_FREE_STOCK, MINICPM5_MK_STATUS_DIR, MINICPM5_MK_PRECOMPILE; and
 MINICPM5_MK_CHECK_POSITIONS=1 cross-checks each fast-path step against the device positions (syncs).
 """
 from __future__ import annotations
@@ -38,7 +38,7 @@ from .config import MkConfig
 from .dispatch import STATE, install_runner_hook, positions_match, scatter_last_rows
 from .mk_weights import prepare_mk_weights
 from .quant import resolve_quant_pair
-from .runtime import WEIGHT_ORDER, MkModel
+from .runtime import WEIGHT_ORDER, MkModel, parse_precompile
 
 logger = logging.getLogger("vllm.minicpm5_mk")
 
@@ -127,6 +127,9 @@ class MiniCPM5MegakernelForCausalLM(LlamaForCausalLM):
                            "backend": "libmk (HIP, gfx950)", "shapes": {}}
         self._mk_write_status()
         logger.info("minicpm5_mk: libmk ready (quant=%s) in %.1fs", quant, time.perf_counter() - t0)
+        # hipGraphs of the listed shapes captured now instead of at each shape's first step (model.py:690-698)
+        self._mk_model.precompile(parse_precompile(os.environ.get("MINICPM5_MK_PRECOMPILE", "")), logits=False,
+                                  log=logger.info)
 
     def _mk_write_status(self) -> None:
         d = os.environ.get("MINICPM5_MK_STATUS_DIR")

@@ -10,6 +10,7 @@ from __future__ import annotations
 
 import ctypes
 import threading
+import time
 
 import torch
 
@@ -29,6 +30,24 @@ def shape_ok(t: torch.Tensor, shape, Lm: int) -> bool:
     if shape == BF16_DUMMY:
         return tuple(t.shape) in ((1,), (Lm, 1))
     return tuple(t.shape) == tuple(shape)
+
+
+def parse_precompile(spec: str) -> list:
+    """MINICPM5_MK_PRECOMPILE's value, e.g. "1x8192,4x8192" -> [(1, 8192), (4, 8192)] (model.py:28, :690-693);
+    empty -> []."""
+    shapes = []
+    for part in (spec or "").split(","):
+        part = part.strip()
+        if not part:
+            continue
+        try:
+            b, s = (int(v) for v in part.lower().split("x"))
+        except ValueError:
+            raise MkError(f"precompile shape {part!r}: expected BxS, e.g. 4x8192") from None
+        if b < 1 or s < 1:
+            raise MkError(f"precompile shape {part!r}: B and S must be positive")
+        shapes.append((b, s))
+    return shapes
 
 
 def _stream():
@@ -146,6 +165,35 @@ class MkModel:
 
     def release_buffers(self) -> None:
         self._bufs.clear()
+
+    def precompile(self, shapes, logits: bool = False, log=None) -> dict:
+        """Captures the hipGraph of every (bs, seq) in `shapes` ahead of its first forward (the reference's
+        MINICPM5_MK_PRECOMPILE, model.py:690-698, which compiles the op per shape at load time).  The
+        graphs are bound to this model's persistent per-shape buffers, which `forward` then reuses, so the
+        first call of a precompiled shape only replays.  Nothing runs on the GPU.  -> {(bs, seq): seconds}"""
+        lib = load()
+        out = {}
+        for bs, seq in shapes:
+            t0 = time.perf_counter()
+            check(lib.mk_validate(ctypes.byref(self.cfg), self.quant.encode(), bs, seq), "mk_validate")
+            if logits and not self.has_lm_head:
+                raise MkError("logits requested but the model was built without lm_head")
+            with self._lock:
+                b = self._buffers(bs, seq, logits)
+                lg = b["logits"]
+                check(lib.mk_precompile(self._h, ctypes.c_void_p(b["ids"].data_ptr()), bs, seq,
+                                        ctypes.c_void_p(b["hidden"].data_ptr()),
+                                        ctypes.c_void_p(lg.data_ptr()) if lg is not None else None,
+                                        ctypes.c_void_p(b["ws"].data_ptr()), b["ws"].numel()), "mk_precompile")
+            out[(bs, seq)] = time.perf_counter() - t0
+            if log:
+                log(f"minicpm5_mk: precompiled {bs}x{seq} in {out[(bs, seq)]:.2f}s")
+        return out
+
+    def graph_count(self) -> int:
+        n = ctypes.c_int()
+        check(load().mk_graph_count(self._h, ctypes.byref(n)), "mk_graph_count")
+        return n.value
 
     def forward(self, input_ids: torch.Tensor, bs: int, seq: int, logits: bool = False, copy_out: bool = True):
         """input_ids (>= bs*seq,) int32/int64 on the GPU, sequence-major -> hidden (max(8, bs), H) bf16

@@ -87,6 +87,17 @@ def test_packed_bytes_arithmetic():
     assert n.value == exp
 
 
+def test_parse_precompile():
+    """MINICPM5_MK_PRECOMPILE's "BxS,BxS" list (model.py:28, :690-693)."""
+    from minicpm5_mk.runtime import MkError, parse_precompile
+
+    assert parse_precompile("") == [] and parse_precompile(None) == []
+    assert parse_precompile("1x8192,4x8192, 32X8192 ,") == [(1, 8192), (4, 8192), (32, 8192)]
+    for bad in ("8192", "1x", "x8192", "1x8192x2", "0x8192", "ax8192"):
+        with pytest.raises(MkError):
+            parse_precompile(bad)
+
+
 def test_sampling_fast_ok_and_eligibility():
     from minicpm5_mk import sampling_fast_ok
     from minicpm5_mk.engine import NotEligible, SamplingParams, eligible_batch, mk_seq_ok

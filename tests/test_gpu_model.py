@@ -414,3 +414,34 @@ def test_runtime_forward_reference_signature(quant):
         runtime.forward(ids_pad, embed, cos, sin, fnorm, *wd, 9, 128, quant, cfg.n_q, cfg.n_kv, cfg.head_dim,
                         cfg.eps, "mystery")
     runtime.clear_cache()
+
+
+@pytest.mark.gpu
+def test_precompile_captures_without_running():
+    """MkModel.precompile (MINICPM5_MK_PRECOMPILE, model.py:690-698) captures one hipGraph per shape
+    without running it: the output buffers keep their contents, the graph count grows by one per new
+    shape, and the first forward of a precompiled shape replays that graph (no new capture) with output
+    bitwise equal to a model that was never precompiled."""
+    from minicpm5_mk.config import preset
+    from minicpm5_mk.engine import MkEngine
+    from minicpm5_mk.synth import random_token_ids
+
+    dev = _dev()
+    cfg = preset("tiny")
+    eng = MkEngine(cfg, quant="auto", max_model_len=1024, device=str(dev), log=lambda *a: None,
+                   precompile="2x256, 1x512")
+    m = eng.model
+    assert m.graph_count() == 2
+    b = m._buffers(2, 256, True)
+    b["hidden"].fill_(7.0)
+    m.precompile([(2, 256)], logits=True)               # cached: no new graph, nothing launched
+    torch.cuda.synchronize()
+    assert m.graph_count() == 2 and bool((b["hidden"] == 7.0).all())
+    ids = random_token_ids(2, 256, seed=5).to(dev)
+    lg = eng.logits(ids).clone()
+    assert m.graph_count() == 2                          # the forward replayed the precompiled graph
+    plain = MkEngine(cfg, quant="auto", max_model_len=1024, device=str(dev), log=lambda *a: None, precompile="")
+    assert plain.model.graph_count() == 0
+    assert torch.equal(lg, plain.logits(ids))
+    eng.close()
+    plain.close()
