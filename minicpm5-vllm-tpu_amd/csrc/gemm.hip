@@ -65,8 +65,10 @@ using CfgX = GemmCfg<256, 256, 2, 4, 4, 1, 1>;
 // 256x192 block, 8 waves of 64x96 (two per SIMD), one workgroup per CU: N = 1536 in 8 column tiles, so
 // M = 8192 fills exactly 256 CUs
 using CfgN = GemmCfg<256, 192, 4, 2, 4, 1, 1>;
-// the same with a 5-stage ring (four stages of loads in flight)
-using CfgN5 = GemmCfg<256, 192, 4, 2, 5, 1, 1>;
+// Short problems (few tiles, each K loop latency-bound): 8-stage rings, seven stages of loads in flight.
+// 128x128 block, 64x64 per wave; 64x128 block, 32x64 per wave; one workgroup per CU
+using CfgD = GemmCfg<128, 128, 2, 2, 8, 1>;
+using CfgE = GemmCfg<64, 128, 2, 2, 8, 1>;
 
 template <GemmIn IN>
 struct Mma;
@@ -262,8 +264,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
   constexpr bool DQ = EPI == Epi::DQ_BF16 || EPI == Epi::DQ2_BF16 || EPI == Epi::DQ_RES_BF16ADD ||
                       EPI == Epi::DQ2_RES_F32ADD || EPI == Epi::DQ2_RES_BF16ADD || EPI == Epi::DQ_SILU ||
                       EPI == Epi::DQ_SILU_F32A || EPI == Epi::SILU_BF16;   // SILU_BF16: only with scales
-  // wave tiles whose width is not a multiple of 64 are processed in 32-column passes
-  constexpr int EW = (SILU || C::WN % 64 == 0) ? C::WN : 32;
+  // the wave's columns are processed in passes of EW = 64 columns (32 when the width is not a multiple
+  // of 64); a SiLU pass is one [32 gate | 32 up] block
+  constexpr int EW = C::WN % 64 == 0 ? 64 : 32;
   constexpr int NSB = C::WN / EW;
   constexpr int TPR = SILU ? EW / 16 : EW / 8;         // tasks per row
   constexpr int TRS = 64 / TPR;                        // rows between a lane's tasks
@@ -272,13 +275,14 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
   static_assert(!SILU || C::WN % 64 == 0, "SiLU epilogue needs whole [gate | up] column blocks per wave");
   const int tcol = lane % TPR, trow0 = lane / TPR;
   const int nb0 = n0 + wn * C::WN;                     // first column of the wave
-  // SiLU: 64-column block blk of the wave is [32 gate | 32 up]; this lane's gate columns start at pg
-  const int pg = SILU ? min(nb0 + (tcol >> 2) * 64, g.N - 64) + (tcol & 3) * 8 : 0;
-  auto pcol = [&](int sb) { return SILU ? pg : min(nb0 + sb * EW + tcol * 8, g.N - 8); };
+  // pass sb: this lane's 8 columns (SiLU: its 8 gate columns; the up columns are 32 further)
+  auto pcol = [&](int sb) {
+    return SILU ? min(nb0 + sb * 64, g.N - 64) + tcol * 8 : min(nb0 + sb * EW + tcol * 8, g.N - 8);
+  };
   const bool dq = DQ && g.rs != nullptr;
   float rsv[C::MT][NTASK];
   f32x4 csv[NSB][SILU ? 4 : 2];
-  if (dq) {
+  auto load_scales = [&] {
 #pragma unroll
     for (int mt = 0; mt < C::MT; ++mt)
 #pragma unroll
@@ -293,7 +297,10 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
         csv[sb][3] = *reinterpret_cast<const f32x4*>(g.cs + pc + 36);
       }
     }
-  }
+  };
+  // the scales are held through the main loop only when they take few registers
+  constexpr bool EARLY_SCALES = C::MT * NTASK + NSB * (SILU ? 16 : 8) <= 32;
+  if (EARLY_SCALES && dq) load_scales();
 
   const int nk = Kb / BKB;
 #pragma unroll
@@ -468,6 +475,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
       }
   };
   if constexpr (RES) load_res(0, rv[0]);
+  if (!EARLY_SCALES && dq) load_scales();
   lds_barrier();   // every wave is done reading the LDS ring
   constexpr int EROW = C::EROW;
   char* er = smem + w * 32 * EROW;
@@ -488,13 +496,15 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
     __builtin_amdgcn_wave_barrier();
     const int mrow0 = m0 + wm * C::WM + mt * 32;
     if constexpr (SILU) {
-      const int blk = tcol >> 2, j0 = (tcol & 3) * 8;
-      const int p0 = nb0 + blk * 64, nh = p0 / 2 + j0;
+      const int j0 = tcol * 8;
+#pragma unroll
+      for (int sb = 0; sb < NSB; ++sb)
 #pragma unroll
       for (int i = 0; i < NTASK; ++i) {
+        const int p0 = nb0 + sb * 64, nh = p0 / 2 + j0;
         const int lr = trow0 + i * TRS, m = mrow0 + lr;
-        const V4* gp = reinterpret_cast<const V4*>(er + lr * EROW + (blk * 64 + j0) * 4);
-        const V4* up = reinterpret_cast<const V4*>(er + lr * EROW + (blk * 64 + 32 + j0) * 4);
+        const V4* gp = reinterpret_cast<const V4*>(er + lr * EROW + (sb * 64 + j0) * 4);
+        const V4* up = reinterpret_cast<const V4*>(er + lr * EROW + (sb * 64 + 32 + j0) * 4);
         const V4 g0 = gp[0], g1 = gp[1], u0 = up[0], u1 = up[1];
         if (m >= g.M || p0 >= g.N) continue;
         float h[8];
@@ -502,8 +512,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
         for (int e = 0; e < 8; ++e) {
           const float gacc = T::f(e < 4 ? g0[e] : g1[e - 4]);
           const float uacc = T::f(e < 4 ? u0[e] : u1[e - 4]);
-          const float sg = dq ? csv[0][e >> 2][e & 3] : 1.f;
-          const float su = dq ? csv[0][2 + (e >> 2)][e & 3] : 1.f;
+          const float sg = dq ? csv[sb][e >> 2][e & 3] : 1.f;
+          const float su = dq ? csv[sb][2 + (e >> 2)][e & 3] : 1.f;
           const float rs = dq ? rsv[mt][i] : 1.f;
           if constexpr (EPI == Epi::SILU_BF16) {
             // XLA path (mk_jax.py:283-299, :420-421): gu rounded to bf16, silu and product in bf16
@@ -667,12 +677,22 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(GemmArgs g, int spli
 // 256x128 workgroups.
 int choose_cfg(const GemmArgs& g) {
   const bool silu = g.epi == Epi::DQ_SILU || g.epi == Epi::DQ_SILU_F32A || g.epi == Epi::SILU_BF16;
-  if (g.cfg >= 1 && g.cfg <= 6 && !(silu && g.cfg >= 5)) return g.cfg;
+  if (g.cfg >= 1 && g.cfg <= 7 && !(silu && g.cfg == 5)) return g.cfg;
   static const int forced = [] {
-    const char* e = std::getenv("MK_GEMM_CFG");   // tuning override: 1 .. 6
+    const char* e = std::getenv("MK_GEMM_CFG");   // tuning override: 1 .. 7
     return e ? std::atoi(e) : 0;
   }();
-  if (forced >= 1 && forced <= 6 && !(silu && forced >= 5)) return forced;
+  if (forced >= 1 && forced <= 7 && !(silu && forced == 5)) return forced;
+  // Few tiles, long K loop (short prompts, e.g. M = 1024 - 2048 with the bf16 O / down projections): each
+  // 64-byte stage costs a memory latency more than its MFMAs, so the deep rings win (measured on MI355X:
+  // the 1B down projection at M = 1024 takes 33.8 us on 64x128, 40.4 on 128x128 deep, 48.4 on the 128x128
+  // three-workgroup tile); with < 64 stages the per-tile fixed cost dominates and the wide tiles stay best.
+  {
+    const int nk = g.K * (g.in == GemmIn::BF16 ? 2 : 1) / BKB;
+    auto tiles = [&](int bm, int bn) { return (long)((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn); };
+    if (nk >= 64 && tiles(64, 128) <= 256) return 7;
+    if (nk >= 64 && tiles(128, 128) <= 256) return 6;
+  }
   struct Opt { int id, bm, bn; double eff; };
   const Opt opts[5] = {{4, 256, 256, silu ? 1.05 : 1.25}, {2, 256, 128, 1.0}, {1, 256, 256, 0.9},
                        {3, 128, 128, 0.85}, {5, 256, 192, 1.15}};
@@ -716,9 +736,8 @@ void launch_t(const GemmArgs& g, hipStream_t st) {
     case 5:
       if constexpr (!silu) launch_c<CfgN, IN, EPI>(g, st);
       break;
-    case 6:
-      if constexpr (!silu) launch_c<CfgN5, IN, EPI>(g, st);
-      break;
+    case 6: launch_c<CfgD, IN, EPI>(g, st); break;
+    case 7: launch_c<CfgE, IN, EPI>(g, st); break;
     default: launch_c<CfgM, IN, EPI>(g, st); break;
   }
 }

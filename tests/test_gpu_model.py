@@ -282,6 +282,26 @@ def test_full_batch_invariance_s8192(name, B):
     m.release_buffers()
 
 
+@pytest.mark.parametrize("name", ["1b", "2b"])
+def test_short_prompt_batch_invariance(name):
+    """Short prompts pick GEMM tiles by problem size: at (1, 1024) and (1, 2048) the bf16 O / down
+    projections run on the deep-ring 64x128 / 128x128 tiles, inside a (4, 1024) batch on the standard
+    ones.  The K summation order is the same on every tile, so each row equals its sequence scored
+    alone, bitwise."""
+    from minicpm5_mk.synth import random_token_ids
+
+    m = _full_model(name)
+    dev = _dev()
+    for S, B in ((1024, 4), (2048, 2)):
+        ids = random_token_ids(B, S, seed=11).to(dev)
+        print(f"[short] {name} ({B}, {S})", flush=True)
+        hB, lB = m.forward(ids.reshape(-1), B, S, logits=True)
+        for b in range(B):
+            h1, l1 = m.forward(ids[b].reshape(-1), 1, S, logits=True, copy_out=False)
+            assert torch.equal(h1[0], hB[b]) and torch.equal(l1[0], lB[b]), f"({B}, {S}) row {b} differs"
+    m.release_buffers()
+
+
 def test_full_model_bf16_1b_hd96_argmax():
     """BASELINE config 1 (1B-hd96): the same model with every linear in bf16 (quant "bf16"), to separate
     the W8A8 numerics from the kernels in the top-1 decision (golden top-1 / top-2 margin 0.029)."""
