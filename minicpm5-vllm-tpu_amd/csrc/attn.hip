@@ -29,7 +29,6 @@ namespace {
 constexpr int QT = 32;   // tokens per q tile (MFMA column block)
 constexpr int KT = 64;   // keys per K/V tile
 constexpr int G = 8;     // q heads per kv head == waves per workgroup
-constexpr int NT = 64 * G;
 
 // Workgroup (32-token block, job, sequence): jobs 0 .. n_kv - 1 RoPE the K of one kv head, jobs n_kv ..
 // 2 n_kv - 1 transpose the V of one.  Small independent workgroups (S / 32 x 2 n_kv per sequence) keep
@@ -145,8 +144,8 @@ __device__ inline float xhalf_sum(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-template <int HD, bool DYN>
-__global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
+template <int HD, bool DYN, int GW>
+__global__ __launch_bounds__(64 * GW, 1) void attn_fwd_kernel(
     const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ cosr,
     const uint16_t* __restrict__ sinr, const uint16_t* __restrict__ krope,
     const uint16_t* __restrict__ vt, uint16_t* __restrict__ out, int B, int S, int n_q, int n_kv,
@@ -164,8 +163,9 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
   const int col = lane & 31, half = lane >> 5;
-  // Work items are (kv head, sequence, 32-token q tile).  Which workgroup computes an item does not
-  // change its result.
+  // Work items are (kv head, group of GW of its G q heads, sequence, 32-token q tile); a wave computes
+  // one q head.  Which workgroup computes an item, and how many heads it shares K / V with (GW), does
+  // not change its result: every wave runs the same instructions on the same data.
   //  * static (!DYN): workgroup = (sequence, kv head, q tiles p and S/32-1-p), so every workgroup does
   //    the same causal work; workgroups are dispatched round-robin over the 8 XCDs (each with its own
   //    L2), and consecutive logical work (same sequence and kv head) is put on one XCD so its L2
@@ -173,10 +173,11 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
   //  * DYN: one persistent workgroup per CU takes items from one queue per kv head (an atomic
   //    counter), longest tiles first: from the queue of its XCD's kv head (XCD id mod n_kv) and, when
   //    that one is empty, from the others.  Used for short or odd-sized launches.
+  constexpr int NHG = G / GW;                        // head groups per kv head
   const int ntiles = S / QT;
-  const int nper = B * ntiles;                       // items per kv head
+  const int nper = B * ntiles * NHG;                 // items per kv head
   const int D = (n_q + 2 * n_kv) * HD;
-  int xq = 0, pair = 0, skv = 0, sb = 0;
+  int xq = 0, pair = 0, skv = 0, sb = 0, shg = 0;
   if constexpr (DYN) {
     unsigned xcc;
     asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
@@ -188,7 +189,8 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
     const int npair = ntiles / 2;
     pair = work % npair;
     skv = (work / npair) % n_kv;
-    sb = work / (npair * n_kv);
+    shg = (work / (npair * n_kv)) % NHG;
+    sb = work / (npair * n_kv * NHG);
   }
   int head = 0;
   __amdgpu_buffer_rsrc_t krs, vrs;   // the item's K and V^T, as buffers for the ring copies
@@ -202,18 +204,18 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
   constexpr int KRC = L::KROW / 16, VRC = L::VROW / 16;
   constexpr int KIN = KT * KRC / 64;                 // instructions per K tile (64 rows: exact)
   constexpr int VIN = (HD * VRC + 63) / 64;          // per V^T tile (the last one partial at hd 96)
-  constexpr int KIW = (KIN + G - 1) / G, VIW = (VIN + G - 1) / G;   // per wave, at most
+  constexpr int KIW = (KIN + GW - 1) / GW, VIW = (VIN + GW - 1) / GW;   // per wave, at most
   static_assert(KT * KRC % 64 == 0, "K image is whole instructions");
   uint32_t koff[KIW], voff[VIW];                     // element offset of this lane's chunk in a tile
 #pragma unroll
   for (int i = 0; i < KIW; ++i) {
-    const int ch = 64 * (w + G * i) + lane;
+    const int ch = 64 * (w + GW * i) + lane;
     const int row = min(ch / KRC, KT - 1), pos = ch % KRC;
     koff[i] = row * HD + (pos < HD / 8 ? pos : 0) * 8;
   }
 #pragma unroll
   for (int i = 0; i < VIW; ++i) {
-    const int ch = 64 * (w + G * i) + lane;
+    const int ch = 64 * (w + GW * i) + lane;
     const int d = min(ch / VRC, HD - 1), pos = ch % VRC;
     voff[i] = d * S + (pos < KT / 8 ? pos : 0) * 8;
   }
@@ -221,16 +223,16 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
     char* dst = kring + slot * L::KBYTES;
 #pragma unroll
     for (int i = 0; i < KIW; ++i) {
-      const int ins = w + G * i;
-      if (KIN % G == 0 || ins < KIN) copy16_to_lds(krs, 2u * (kt * KT * HD + koff[i]), dst + 1024 * ins);
+      const int ins = w + GW * i;
+      if (KIN % GW == 0 || ins < KIN) copy16_to_lds(krs, 2u * (kt * KT * HD + koff[i]), dst + 1024 * ins);
     }
   };
   auto aload_v = [&](int kt, int slot) {
     char* dst = vring + slot * L::VBYTES;
 #pragma unroll
     for (int i = 0; i < VIW; ++i) {
-      const int ins = w + G * i;
-      if (VIN % G == 0 || ins < VIN) {
+      const int ins = w + GW * i;
+      if (VIN % GW == 0 || ins < VIN) {
         if (HD * VRC % 64 == 0 || 64 * ins + lane < HD * VRC)
           copy16_to_lds(vrs, 2u * (kt * KT + voff[i]), dst + 1024 * ins);
       }
@@ -238,7 +240,7 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
   };
 
   for (int pass = 0;; ++pass) {
-    int kv, qt, b;
+    int kv, qt, b, hg;
     if constexpr (DYN) {
       if (tid == 0) {
         int it = -1;
@@ -256,15 +258,18 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
       const int item = *item_s;
       if (item < 0) break;
       kv = item / nper;
-      qt = ntiles - 1 - (item % nper) / B;
-      b = (item % nper) % B;
+      const int v = item % nper;                     // longest tiles first
+      qt = ntiles - 1 - v / (B * NHG);
+      hg = (v % (B * NHG)) / B;
+      b = v % B;
     } else {
       if (pass == 2) break;
       kv = skv;
       b = sb;
+      hg = shg;
       qt = pass == 0 ? pair : ntiles - 1 - pair;
     }
-    head = kv * G + w;
+    head = kv * G + hg * GW + w;
     krs = make_rsrc(krope + ((size_t)b * n_kv + kv) * (size_t)S * HD, S * HD * 2);
     vrs = make_rsrc(vt + ((size_t)b * n_kv + kv) * (size_t)HD * S, S * HD * 2);
     const int t0 = qt * QT;
@@ -576,16 +581,24 @@ int launch_attn_hd(const AttnArgs& a, hipStream_t st, int stages) {
         n = 0;
       return n > 0 ? n : 256;
     }();
-    // static pairs when they fill the CUs in whole rounds (no queue atomics, fixed XCD placement),
-    // else the work queues
-    const int items = a.B * a.n_kv * (a.S / QT), pairs = items / 2;
-    if (pairs % ncu == 0) {
-      hipLaunchKernelGGL((attn_fwd_kernel<HD, false>), dim3(pairs), dim3(NT), 0, st, a.qkv, a.cos, a.sin,
-                         a.krope, a.vt, a.out, a.B, a.S, a.n_q, a.n_kv, a.qscale, queue);
-    } else {
-      hipLaunchKernelGGL((attn_fwd_kernel<HD, true>), dim3(items < ncu ? items : ncu), dim3(NT), 0, st, a.qkv,
-                         a.cos, a.sin, a.krope, a.vt, a.out, a.B, a.S, a.n_q, a.n_kv, a.qscale, queue);
-    }
+    // Workgroups of 8 waves (the kv head's 8 q heads share every K / V tile) when there is an item for
+    // every CU, else of 4 (twice the items, one wave per SIMD: the longest q tile finishes sooner).  Static
+    // pairs when they fill the CUs in whole rounds (no queue atomics, fixed XCD placement), else the work
+    // queues.
+    const int items8 = a.B * a.n_kv * (a.S / QT);
+    auto go = [&](auto gw) {
+      constexpr int GW = decltype(gw)::value;
+      const int items = items8 * (G / GW), pairs = items / 2;
+      if (pairs % ncu == 0) {
+        hipLaunchKernelGGL((attn_fwd_kernel<HD, false, GW>), dim3(pairs), dim3(64 * GW), 0, st, a.qkv, a.cos,
+                           a.sin, a.krope, a.vt, a.out, a.B, a.S, a.n_q, a.n_kv, a.qscale, queue);
+      } else {
+        hipLaunchKernelGGL((attn_fwd_kernel<HD, true, GW>), dim3(items < ncu ? items : ncu), dim3(64 * GW), 0, st,
+                           a.qkv, a.cos, a.sin, a.krope, a.vt, a.out, a.B, a.S, a.n_q, a.n_kv, a.qscale, queue);
+      }
+    };
+    if (items8 < ncu) go(std::integral_constant<int, 4>{});
+    else go(std::integral_constant<int, G>{});
     MK_HIP_CHECK(hipGetLastError());
   }
   return MK_OK;
