@@ -122,6 +122,12 @@ int mk_forward(mk_model* m, const int32_t* input_ids, int bs, int seq, void* hid
 int mk_precompile(mk_model* m, const int32_t* input_ids, int bs, int seq, void* hidden_out, float* logits_out,
                   void* workspace, size_t workspace_bytes);
 
+/* 1 (default): the QKV projection's epilogue writes the attention's RoPE'd K and transposed V (no
+ * separate prep launch); 0: a prep kernel does it after the projection (the layout of work of the
+ * reference's kernel, mk_attn.py:568-580).  Results are identical; 0 exists to check that.  Drops the
+ * cached graphs when it changes. */
+int mk_set_attn_prep_fused(mk_model* m, int enable);
+
 /* Number of hipGraphs the model holds (at most 16: the least recently captured is dropped first). */
 int mk_graph_count(const mk_model* m, int* n);
 
@@ -253,7 +259,9 @@ int mk_weight_quantize(const void* w, int n_out, int n_in, float fold, const flo
 
 /* Weight repack (used by mk_model_create; exported for tests): out (N, K) = in (K, N)^T.
  * map 1: N == 2 * inter columns in the reference's gate/up layout with chunk ic, reordered into
- * 32-column gate/up interleave blocks. */
+ * 32-column gate/up interleave blocks.
+ * map 2: the QKV projection, ic = q columns, inter = head dim: q and v columns in order, each K head's
+ * columns in 8-column RoPE pair groups [4g .. 4g+3 | hd/2 + 4g .. hd/2 + 4g + 3]. */
 int mk_pack_weight(const void* in, int ld_in, void* out, int K, int N, int elem_bytes, int map, int ic,
                    int inter, void* stream);
 

@@ -131,6 +131,16 @@ int mk_precompile(mk_model* m, const int32_t* input_ids, int bs, int seq, void* 
   MK_TRY(mk::model_precompile(m->impl, input_ids, bs, seq, hidden_out, logits_out, workspace, workspace_bytes));
 }
 
+int mk_set_attn_prep_fused(mk_model* m, int enable) {
+  MK_REQUIRE(m != nullptr, "set_attn_prep_fused: null model");
+  if (m->impl->fuse_prep != (enable != 0)) {   // captured graphs hold the old launch sequence
+    for (auto& g : m->impl->graphs) hipGraphExecDestroy(g.exec);
+    m->impl->graphs.clear();
+  }
+  m->impl->fuse_prep = enable != 0;
+  return MK_OK;
+}
+
 int mk_graph_count(const mk_model* m, int* n) {
   MK_REQUIRE(m != nullptr && n != nullptr, "graph_count: null argument");
   *n = (int)m->impl->graphs.size();
@@ -336,6 +346,8 @@ int mk_pack_weight(const void* in, int ld_in, void* out, int K, int N, int elem_
   p.map = map;
   p.ic = ic;
   p.inter = inter;
+  p.qd = ic;      // map 2: ic = q columns, inter = head dim
+  p.hd = inter;
   MK_TRY(mk::launch_pack(p, static_cast<hipStream_t>(stream)));
 }
 

@@ -41,7 +41,7 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(const uint16_t* __restri
                                                         const uint16_t* __restrict__ sinr,
                                                         uint16_t* __restrict__ krope,
                                                         uint16_t* __restrict__ vt, int S, int n_q,
-                                                        int n_kv, int* __restrict__ queue) {
+                                                        int n_kv, int* __restrict__ queue, int k_pairs) {
   // the attention kernel's work queues start empty (vector atomics: no scalar-cache writes)
   if (blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && threadIdx.x <= n_kv) atomicExch(&queue[threadIdx.x], 0);
   const int t0 = blockIdx.x * PT, job = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
@@ -57,8 +57,18 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(const uint16_t* __restri
       const int t = idx / NC, c = idx % NC;
       const uint16_t* kr = base + (size_t)t * D + (n_q + kv) * HD;
       const size_t tb = (size_t)(t0 + t) * HD;
-      const u32x4 lo = *reinterpret_cast<const u32x4*>(kr + 8 * c);
-      const u32x4 hi = *reinterpret_cast<const u32x4*>(kr + H2 + 8 * c);
+      u32x4 lo, hi;
+      if (k_pairs) {
+        // K columns in RoPE pair groups (pack.hip map 2): packed columns 16 c .. 16 c + 15 hold dims
+        // 8 c + {0..3}, H2 + 8 c + {0..3}, 8 c + {4..7}, H2 + 8 c + {4..7}
+        const u32x4 a = *reinterpret_cast<const u32x4*>(kr + 16 * c);
+        const u32x4 b = *reinterpret_cast<const u32x4*>(kr + 16 * c + 8);
+        lo = u32x4{a[0], a[1], b[0], b[1]};
+        hi = u32x4{a[2], a[3], b[2], b[3]};
+      } else {
+        lo = *reinterpret_cast<const u32x4*>(kr + 8 * c);
+        hi = *reinterpret_cast<const u32x4*>(kr + H2 + 8 * c);
+      }
       const u32x4 cl = *reinterpret_cast<const u32x4*>(cosr + tb + 8 * c);
       const u32x4 ch = *reinterpret_cast<const u32x4*>(cosr + tb + H2 + 8 * c);
       const u32x4 sl = *reinterpret_cast<const u32x4*>(sinr + tb + 8 * c);
@@ -66,9 +76,11 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(const uint16_t* __restri
       u32x4 olo, ohi;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float x1a = bf_lo(lo[e]), x1b = bf_hi(lo[e]), x2a = bf_lo(hi[e]), x2b = bf_hi(hi[e]);
-        olo[e] = pack_bf2(x1a * bf_lo(cl[e]) - x2a * bf_lo(sl[e]), x1b * bf_hi(cl[e]) - x2b * bf_hi(sl[e]));
-        ohi[e] = pack_bf2(x2a * bf_lo(ch[e]) + x1a * bf_lo(sh[e]), x2b * bf_hi(ch[e]) + x1b * bf_hi(sh[e]));
+        float la, ha, lb, hb;
+        rope_pair(bf_lo(lo[e]), bf_lo(hi[e]), bf_lo(cl[e]), bf_lo(sl[e]), bf_lo(ch[e]), bf_lo(sh[e]), la, ha);
+        rope_pair(bf_hi(lo[e]), bf_hi(hi[e]), bf_hi(cl[e]), bf_hi(sl[e]), bf_hi(ch[e]), bf_hi(sh[e]), lb, hb);
+        olo[e] = pack_bf2(la, lb);
+        ohi[e] = pack_bf2(ha, hb);
       }
       *reinterpret_cast<u32x4*>(kdst + (size_t)t * HD + 8 * c) = olo;
       *reinterpret_cast<u32x4*>(kdst + (size_t)t * HD + H2 + 8 * c) = ohi;
@@ -559,18 +571,13 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_fwd_kernel(
   }
 }
 
-// work-queue counters (n_kv item counters + a done counter) after K and V^T in the scratch
-inline int* attn_queue(const AttnArgs& a) {
-  return reinterpret_cast<int*>(a.vt + (size_t)a.B * a.n_kv * a.hd * a.S);
-}
-
 template <int HD>
 int launch_attn_hd(const AttnArgs& a, hipStream_t st, int stages) {
   int* queue = attn_queue(a);
   if (stages & 1) {
     const dim3 pg(a.S / PT, 2 * a.n_kv, a.B);
     hipLaunchKernelGGL(attn_prep_kernel<HD>, pg, dim3(256), 0, st, a.qkv, a.cos, a.sin, a.krope, a.vt,
-                       a.S, a.n_q, a.n_kv, queue);
+                       a.S, a.n_q, a.n_kv, queue, a.k_pairs);
     MK_HIP_CHECK(hipGetLastError());
   }
   if (stages & 2) {

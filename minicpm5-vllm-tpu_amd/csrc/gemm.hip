@@ -162,6 +162,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index, kept in an SGPR
+  constexpr bool ROUTE = EPI == Epi::DQ_BF16 || EPI == Epi::DQ2_BF16 || EPI == Epi::BF16;
+  // QKV routing: the attention's work queues start empty (vector atomics: no scalar-cache writes)
+  if (ROUTE && g.queue && blockIdx.x == 0 && blockIdx.y == 0 && tid <= g.n_kv) atomicExch(&g.queue[tid], 0);
   const int col = lane & 31, half = lane >> 5;
   const int wm = w / C::WGN, wn = w % C::WGN;
   // Tile order.  Workgroups are dispatched round-robin over the 8 XCDs, each with its own L2: launch id
@@ -542,7 +545,96 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
       }
     } else {
 #pragma unroll
-      for (int sb = 0; sb < NSB; ++sb)
+      for (int sb = 0; sb < NSB; ++sb) {
+      if constexpr (ROUTE) {
+        // QKV routing (q, K and V blocks start at multiples of 64 columns, so a pass is all one of them).
+        // V columns: lane task =
+        // (column, 8 consecutive V^T positions of the slice) -> one 16-byte chunk of a V^T row, read from
+        // the staged slice by column (positions p hold tokens vt_key_pos(p), in two runs of 4 rows)
+        const int pc0 = nb0 + sb * EW, vcol0 = g.qd + g.n_kv * g.hd;
+        if (g.krope && pc0 >= g.qd && pc0 < vcol0) {
+          // K columns (packed in RoPE pair groups, pack.hip map 2): the usual task layout, each task four
+          // (d, d + hd/2) pairs of one head at one token, rounded to bf16 and RoPE'd exactly as the
+          // attention's prep kernel does it; the table entries of every task are loaded first
+          if (mrow0 < g.M) {
+            const int b = mrow0 / g.S, t0 = mrow0 - b * g.S;
+            const int n = pc0 + tcol * 8, r = n - g.qd, kv = r / g.hd, d = ((r - kv * g.hd) / 8) * 4;
+            u32x2 c1[NTASK], c2[NTASK], s1[NTASK], s2[NTASK];
+#pragma unroll
+            for (int i = 0; i < NTASK; ++i) {
+              const size_t tb = (size_t)(t0 + trow0 + i * TRS) * g.hd;
+              c1[i] = *reinterpret_cast<const u32x2*>(g.cos + tb + d);
+              c2[i] = *reinterpret_cast<const u32x2*>(g.cos + tb + g.hd / 2 + d);
+              s1[i] = *reinterpret_cast<const u32x2*>(g.sin + tb + d);
+              s2[i] = *reinterpret_cast<const u32x2*>(g.sin + tb + g.hd / 2 + d);
+            }
+#pragma unroll
+            for (int i = 0; i < NTASK; ++i) {
+              const int lr = trow0 + i * TRS;
+              const V4* vp = reinterpret_cast<const V4*>(er + lr * EROW + (sb * EW + tcol * 8) * 4);
+              const V4 q0 = vp[0], q1 = vp[1];
+              float v[8];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                v[e] = T::f(q0[e]);
+                v[4 + e] = T::f(q1[e]);
+              }
+              if constexpr (DQ) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                  const float cs = csv[sb][e >> 2][e & 3];
+                  if constexpr (EPI == Epi::DQ2_BF16) v[e] = v[e] * (rsv[mt][i] * cs);
+                  else v[e] = (v[e] * rsv[mt][i]) * cs;
+                }
+              }
+              float lo[4], hi[4];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const int wd = e >> 1;
+                auto bf = [&](uint32_t x) { return e & 1 ? bf_hi(x) : bf_lo(x); };
+                rope_pair(bf2f(f2bf(v[e])), bf2f(f2bf(v[4 + e])), bf(c1[i][wd]), bf(s1[i][wd]), bf(c2[i][wd]),
+                          bf(s2[i][wd]), lo[e], hi[e]);
+              }
+              uint16_t* kd = g.krope + (((size_t)b * g.n_kv + kv) * g.S + t0 + lr) * g.hd;
+              *reinterpret_cast<u32x2*>(kd + d) = u32x2{pack_bf2(lo[0], lo[1]), pack_bf2(lo[2], lo[3])};
+              *reinterpret_cast<u32x2*>(kd + g.hd / 2 + d) = u32x2{pack_bf2(hi[0], hi[1]), pack_bf2(hi[2], hi[3])};
+            }
+          }
+          continue;
+        }
+        if (g.krope && pc0 >= vcol0) {
+          if (mrow0 < g.M) {
+            const int b = mrow0 / g.S, t0 = mrow0 - b * g.S;
+#pragma unroll
+            for (int k = 0; k < EW * 4 / 64; ++k) {
+              const int task = lane + 64 * k, cc = task % EW, p0 = 8 * (task / EW);
+              const int n = pc0 + cc;
+              if (n >= g.N) continue;
+              const int ra = vt_key_pos(p0), rb = vt_key_pos(p0 + 4);   // rows ra .. ra+3, rb .. rb+3
+              float v[8];
+#pragma unroll
+              for (int e = 0; e < 8; ++e)
+                v[e] = T::f(*reinterpret_cast<const typename T::Elem*>(er + ((e < 4 ? ra : rb) + (e & 3)) * EROW +
+                                                                       (sb * EW + cc) * 4));
+              if constexpr (DQ) {
+                const f32x4 sa = *reinterpret_cast<const f32x4*>(g.rs + mrow0 + ra);
+                const f32x4 sb4 = *reinterpret_cast<const f32x4*>(g.rs + mrow0 + rb);
+                const float cs = g.cs[n];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                  const float rsm = e < 4 ? sa[e] : sb4[e - 4];
+                  if constexpr (EPI == Epi::DQ2_BF16) v[e] = v[e] * (rsm * cs);
+                  else v[e] = (v[e] * rsm) * cs;
+                }
+              }
+              const int r2 = n - vcol0, kv = r2 / g.hd, d = r2 - kv * g.hd;
+              *reinterpret_cast<u32x4*>(g.vt + (((size_t)b * g.n_kv + kv) * g.hd + d) * g.S + t0 + p0) =
+                  u32x4{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]), pack_bf2(v[4], v[5]), pack_bf2(v[6], v[7])};
+            }
+          }
+          continue;
+        }
+      }
 #pragma unroll
       for (int i = 0; i < NTASK; ++i) {
         const int c8 = sb * EW + tcol * 8, n = nb0 + c8;
@@ -595,6 +687,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
         }
         uint16_t* op = RES ? g.res + (size_t)m * g.ldr + n : static_cast<uint16_t*>(g.out) + (size_t)m * g.ldo + n;
         *reinterpret_cast<u32x4*>(op) = o;
+      }
       }
     }
     __builtin_amdgcn_wave_barrier();
@@ -869,6 +962,19 @@ int launch_gemm(const GemmArgs& g, hipStream_t st) {
   MK_REQUIRE(((uintptr_t)g.out % 16) == 0 && ((uintptr_t)g.res % 16) == 0 && ((uintptr_t)g.cs % 16) == 0 &&
                  ((uintptr_t)g.aux % 16) == 0,
              "gemm: output, residual and scale vectors must be 16-byte aligned");
+  if (g.krope) {
+    MK_REQUIRE(g.epi == Epi::DQ_BF16 || g.epi == Epi::DQ2_BF16 || g.epi == Epi::BF16,
+               "gemm: QKV routing needs the DQ_BF16, DQ2_BF16 or BF16 epilogue");
+    MK_REQUIRE(g.vt && g.cos && g.sin && g.hd >= 8 && g.hd % 8 == 0 && g.n_kv >= 1 && g.qd >= 0 && g.qd % 8 == 0 &&
+                   g.N == g.qd + 2 * g.n_kv * g.hd && g.qd % 64 == 0 && (g.qd + g.n_kv * g.hd) % 64 == 0 &&
+                   g.S % 32 == 0 &&
+                   g.M % g.S == 0,
+               "gemm: QKV routing needs N = qd + 2 n_kv hd with the K and V blocks at multiples of 64 columns, hd % 8 "
+               "== 0 and whole sequences of S rows (S % 32 == 0)");
+    MK_REQUIRE(((uintptr_t)g.krope % 16) == 0 && ((uintptr_t)g.vt % 16) == 0 && ((uintptr_t)g.cos % 16) == 0 &&
+                   ((uintptr_t)g.sin % 16) == 0,
+               "gemm: QKV routing buffers must be 16-byte aligned");
+  }
   switch (g.in) {
     case GemmIn::I8: return dispatch<GemmIn::I8>(g, st, false);
     case GemmIn::F8: return dispatch<GemmIn::F8>(g, st, false);
@@ -880,6 +986,7 @@ int launch_gemm_skinny(const GemmArgs& g, hipStream_t st) {
   int rc = gemm_validate(g);
   if (rc) return rc;
   MK_REQUIRE(g.M <= 32, "gemm_skinny: M must be <= 32");
+  MK_REQUIRE(!g.krope, "gemm_skinny: no QKV routing");
   switch (g.in) {
     case GemmIn::I8: return dispatch<GemmIn::I8>(g, st, true);
     case GemmIn::F8: return dispatch<GemmIn::F8>(g, st, true);

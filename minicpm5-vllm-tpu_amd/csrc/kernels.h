@@ -17,6 +17,7 @@ struct AttnArgs {
   uint16_t* out;         // (B, S, n_q hd) bf16
   int B, S, n_q, n_kv, hd;
   float qscale;          // multiplies RoPE'd q before the bf16 rounding (sm_scale * log2 e)
+  int k_pairs;           // 1: qkv's K columns are in RoPE pair groups (pack.hip map 2), 0: the reference order
 };
 int attn_validate(int B, int S, int n_q, int n_kv, int hd);
 size_t attn_scratch_bytes(int B, int S, int n_kv, int hd);
@@ -24,6 +25,10 @@ int launch_attn(const AttnArgs& a, hipStream_t st);
 // stages: 1 = K-RoPE / V-transpose prep (also empties the work queues), 2 = the attention kernel
 // (leaves the queues empty for the next launch), 3 = both
 int launch_attn_stages(const AttnArgs& a, hipStream_t st, int stages);
+// The attention's work-queue counters (n_kv item counters + a done counter) after V^T in the scratch.
+inline int* attn_queue(const AttnArgs& a) {
+  return reinterpret_cast<int*>(a.vt + (size_t)a.B * a.n_kv * a.hd * a.S);
+}
 
 // Last-token attention of the last layer (mk_jax.py:492-520): one query per sequence over all S keys.
 struct LastAttnArgs {
@@ -73,6 +78,17 @@ struct GemmArgs {
   int gm;                     // tile-order group height (rows of tiles); 0 = chosen by the launcher
   void* ws;                   // skinny GEMM: optional f32 workspace for split-K partials (null = no split)
   size_t ws_bytes;
+  // QKV routing (does the attention's prep work in the QKV projection's epilogue; DQ_BF16, DQ2_BF16 and
+  // BF16 only): with krope set, output columns [qd, qd + n_kv hd) -- K, packed in RoPE pair groups
+  // (pack.hip map 2) -- are rounded to bf16, RoPE'd at token m % S and stored to krope (B, n_kv, S, hd);
+  // columns [qd + n_kv hd, N) -- V -- to vt (B, n_kv, hd, S) in the PV operand's key order; q columns go
+  // to out as usual; queue[0 .. n_kv] is zeroed.
+  uint16_t* krope;
+  uint16_t* vt;
+  const uint16_t* cos;
+  const uint16_t* sin;
+  int* queue;
+  int S, hd, qd, n_kv;
 };
 int gemm_validate(const GemmArgs& g);
 int launch_gemm(const GemmArgs& g, hipStream_t st);
@@ -126,11 +142,14 @@ struct PackArgs {
   void* out;                      // (N, K) destination, row-major
   int K, N;
   int elem;                       // bytes per element (1 or 2)
-  int map;                        // 0: identity, 1: gate/up 32-interleave from chunk layout
+  int map;                        // 0: identity, 1: gate/up 32-interleave from chunk layout,
+                                  // 2: QKV with each K head in RoPE pair groups (pack.hip)
   int ic, inter;                  // map 1 parameters
+  int qd, hd;                     // map 2 parameters: q columns, head dim
 };
 int launch_pack(const PackArgs& p, hipStream_t st);
-int launch_pack_scales(const float* in, float* out, int inter, int ic, hipStream_t st);
+// out[p] = in[source column of p] for the N columns of a per-column vector (scales), map as in p
+int launch_pack_cols(const float* in, float* out, const PackArgs& p, hipStream_t st);
 
 // ------------------------------------------------------------------------------ weight preparation
 // HF weight w (n_out, n_in) bf16, W = w^T * fold (in, out) f32 (prep.hip):

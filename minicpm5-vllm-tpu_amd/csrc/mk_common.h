@@ -46,6 +46,18 @@ __device__ inline uint32_t pack_bf2(float a, float b) {
 __device__ inline float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ inline float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
+// RoPE (rotate-half) of the dim pair (d, d + hd/2) of one token, f32 products of the bf16 values x1 = x[d],
+// x2 = x[d + hd/2] and table entries c1, s1 at d and c2, s2 at d + hd/2.  One definition for every kernel
+// that RoPEs K, so all of them round alike.
+__device__ inline void rope_pair(float x1, float x2, float c1, float s1, float c2, float s2, float& lo, float& hi) {
+  lo = x1 * c1 - x2 * s1;
+  hi = x2 * c2 + x1 * s2;
+}
+
+// Key position inside a 16-key group of V^T rows: bits 2 and 3 of the key index swapped, so the 8 keys
+// a lane's P^T column covers in the attention kernel are one 16-byte chunk (an involution).
+__device__ __host__ inline int vt_key_pos(int t) { return (t & ~12) | ((t & 4) << 1) | ((t & 8) >> 1); }
+
 template <typename T>
 __device__ inline T bitcast(const u32x4& v) {
   T r;

@@ -148,6 +148,7 @@ int packed_layout(const mk_config* c, const QuantPlan& q, PackedLayout* L) {
     return o;
   };
   L->wqkv = take(Lm * D * H * esz(q.i8[0]));
+  L->sqkv = take(q.i8[0] ? Lm * D * sizeof(float) : 0);
   L->wo = take(Lm * H * qd * esz(q.i8[1]));
   L->wgu = take(Lm * 2 * I * H * esz(q.i8[2]));
   L->sgu = take(q.i8[2] ? Lm * 2 * I * sizeof(float) : 0);
@@ -257,6 +258,8 @@ int model_create(const mk_config* cfg, const char* quant, const mk_weights* w, v
       p.map = map;
       p.ic = ic;
       p.inter = I;
+      p.qd = qd;
+      p.hd = cfg->head_dim;
       int r = launch_pack(p, st);
       if (r) return r;
     }
@@ -264,14 +267,31 @@ int model_create(const mk_config* cfg, const char* quant, const mk_weights* w, v
   };
   char* pb = m->packed;
   const int e0 = (int)esz(q.i8[0]), e1 = (int)esz(q.i8[1]), e2 = (int)esz(q.i8[2]), e3 = (int)esz(q.i8[3]);
-  if ((rc = pack(w->w_qkv, (size_t)H * D * e0, H, D, e0, 0, pb + P.wqkv, (size_t)D * H * e0, Lm))) return fail(rc);
+  // QKV rows in RoPE pair order: the projection's epilogue applies K's RoPE (pack.hip)
+  if ((rc = pack(w->w_qkv, (size_t)H * D * e0, H, D, e0, 2, pb + P.wqkv, (size_t)D * H * e0, Lm))) return fail(rc);
+  if (q.i8[0]) {
+    PackArgs pc{};
+    pc.N = D;
+    pc.map = 2;
+    pc.qd = qd;
+    pc.hd = cfg->head_dim;
+    for (int l = 0; l < Lm; ++l) {
+      rc = launch_pack_cols(w->s_qkv + (size_t)l * D, reinterpret_cast<float*>(pb + P.sqkv) + (size_t)l * D, pc, st);
+      if (rc) return fail(rc);
+    }
+  }
   if ((rc = pack(w->w_o, (size_t)qd * H * e1, qd, H, e1, 0, pb + P.wo, (size_t)H * qd * e1, Lm))) return fail(rc);
   if ((rc = pack(w->w_gu, (size_t)H * 2 * I * e2, H, 2 * I, e2, 1, pb + P.wgu, (size_t)2 * I * H * e2, Lm)))
     return fail(rc);
   if (q.i8[2]) {
+    PackArgs pc{};
+    pc.N = 2 * I;
+    pc.map = 1;
+    pc.ic = ic;
+    pc.inter = I;
     for (int l = 0; l < Lm; ++l) {
-      rc = launch_pack_scales(w->s_gu + (size_t)l * 2 * I, reinterpret_cast<float*>(pb + P.sgu) + (size_t)l * 2 * I, I,
-                              ic, st);
+      rc = launch_pack_cols(w->s_gu + (size_t)l * 2 * I, reinterpret_cast<float*>(pb + P.sgu) + (size_t)l * 2 * I, pc,
+                            st);
       if (rc) return fail(rc);
     }
   }
@@ -369,40 +389,8 @@ int launch_forward(const Fwd& f, hipStream_t st) {
   MK_RUN(launch_embed(f.ids, static_cast<const uint16_t*>(m.w.embed), x, T, H, c.vocab, st));
 
   for (int l = 0; l < Lm; ++l) {
-    // ---- RMSNorm + QKV projection (_qkv_block, mk_jax.py:398-405)
-    GemmArgs g{};
-    g.M = T;
-    g.N = D;
-    g.K = H;
-    g.lda = H;
-    g.ldb = H;
-    g.out = qkv;
-    g.ldo = D;
-    g.B = pb + m.P.wqkv + (size_t)l * D * H * e0;
-    if (q.i8[0]) {
-      QuantArgs qa = act_quant(q.mode[0], true, false, x, H, m.w.a_qkv + (size_t)l * H, T, H, c.eps, xq, sx);
-      if (q.fqkv) {   // fused_qkv prologue (mk_mlp.py:161-168)
-        qa.recip = true;
-        qa.smul = true;
-      }
-      kind = MK_KERNEL_NORM;
-      MK_RUN(launch_rowquant(qa, st));
-      g.in = fp8(q.mode[0]) ? GemmIn::F8 : GemmIn::I8;
-      g.A = xq;
-      g.rs = sx;
-      g.cs = m.w.s_qkv + (size_t)l * D;
-      g.epi = q.fqkv ? Epi::DQ_BF16 : Epi::DQ2_BF16;
-    } else {
-      kind = MK_KERNEL_NORM;
-      MK_RUN(launch_rmsnorm_bf16(x, H, nullptr, xn, H, T, H, c.eps, st));
-      g.in = GemmIn::BF16;
-      g.A = xn;
-      g.epi = Epi::BF16;
-    }
-    kind = MK_KERNEL_GEMM_QKV;
-    MK_RUN(launch_gemm(g, st));
-
-    // ---- causal GQA attention (super_gqa_v2); sm_scale is folded into W_q (mk_weights.py:147)
+    // ---- RMSNorm + QKV projection (_qkv_block, mk_jax.py:398-405), then the causal GQA attention
+    // (super_gqa_v2); sm_scale is folded into W_q (mk_weights.py:147)
     AttnArgs aa{};
     aa.qkv = qkv;
     aa.cos = cosr;
@@ -416,8 +404,54 @@ int launch_forward(const Fwd& f, hipStream_t st) {
     aa.n_kv = c.n_kv;
     aa.hd = c.head_dim;
     aa.qscale = 1.4426950408889634f;
-    kind = MK_KERNEL_ATTN_PREP;
-    MK_RUN(launch_attn_stages(aa, st, 1));
+    aa.k_pairs = 1;   // W_qkv is packed with K in RoPE pair groups
+
+    GemmArgs g{};
+    g.M = T;
+    g.N = D;
+    g.K = H;
+    g.lda = H;
+    g.ldb = H;
+    g.out = qkv;
+    g.ldo = D;
+    g.B = pb + m.P.wqkv + (size_t)l * D * H * e0;
+    if (m.fuse_prep) {   // the QKV epilogue writes the attention's RoPE'd K and V^T (and empties its queues)
+      g.krope = aa.krope;
+      g.vt = aa.vt;
+      g.cos = cosr;
+      g.sin = sinr;
+      g.queue = attn_queue(aa);
+      g.S = S;
+      g.hd = c.head_dim;
+      g.qd = qd;
+      g.n_kv = c.n_kv;
+    }
+    if (q.i8[0]) {
+      QuantArgs qa = act_quant(q.mode[0], true, false, x, H, m.w.a_qkv + (size_t)l * H, T, H, c.eps, xq, sx);
+      if (q.fqkv) {   // fused_qkv prologue (mk_mlp.py:161-168)
+        qa.recip = true;
+        qa.smul = true;
+      }
+      kind = MK_KERNEL_NORM;
+      MK_RUN(launch_rowquant(qa, st));
+      g.in = fp8(q.mode[0]) ? GemmIn::F8 : GemmIn::I8;
+      g.A = xq;
+      g.rs = sx;
+      g.cs = reinterpret_cast<const float*>(pb + m.P.sqkv) + (size_t)l * D;   // s_qkv in the packed column order
+      g.epi = q.fqkv ? Epi::DQ_BF16 : Epi::DQ2_BF16;
+    } else {
+      kind = MK_KERNEL_NORM;
+      MK_RUN(launch_rmsnorm_bf16(x, H, nullptr, xn, H, T, H, c.eps, st));
+      g.in = GemmIn::BF16;
+      g.A = xn;
+      g.epi = Epi::BF16;
+    }
+    kind = MK_KERNEL_GEMM_QKV;
+    MK_RUN(launch_gemm(g, st));
+    if (!m.fuse_prep) {
+      kind = MK_KERNEL_ATTN_PREP;
+      MK_RUN(launch_attn_stages(aa, st, 1));
+    }
     kind = MK_KERNEL_ATTN;
     MK_RUN(launch_attn_stages(aa, st, 2));
 

@@ -20,7 +20,7 @@ struct QuantPlan {
 
 // Byte offsets of the packed (K-contiguous) weights inside the caller's packed buffer.
 struct PackedLayout {
-  size_t wqkv, wo, wgu, sgu, wd, wlqkv, wlo, wlgu, wld, total;
+  size_t wqkv, sqkv, wo, wgu, sgu, wd, wlqkv, wlo, wlgu, wld, total;
 };
 
 // Byte offsets of the forward's buffers inside the caller's workspace.
@@ -53,6 +53,7 @@ struct Model {
   char* packed = nullptr;
   bool use_graph = true;
   int max_chunk = 0;   // caller's cap on sequences per chunk (0: only the 4 GiB operand limit)
+  bool fuse_prep = true;   // K RoPE / V^T written by the QKV projection's epilogue (else the prep kernel)
   hipStream_t cap_stream = nullptr;
   std::vector<CachedGraph> graphs;
   ~Model();

@@ -54,6 +54,7 @@ SIGNATURES = {
     "mk_set_graph_mode": (_I, [_P, _I]),
     "mk_precompile": (_I, [_P, _P, _I, _I, _P, _P, _P, _SZ]),
     "mk_graph_count": (_I, [_P, ctypes.POINTER(_I)]),
+    "mk_set_attn_prep_fused": (_I, [_P, _I]),
     "mk_set_max_chunk": (_I, [_P, _I]),
     "mk_forward_timed": (_I, [_P, _P, _I, _I, _P, _P, _P, _SZ, _P, _P, _P]),
     "mk_attn_scratch_bytes": (_SZ, [_I, _I, _I, _I]),

@@ -140,6 +140,11 @@ class MkModel:
     def set_graph_mode(self, enable: bool) -> None:
         check(load().mk_set_graph_mode(self._h, int(enable)), "mk_set_graph_mode")
 
+    def set_attn_prep_fused(self, enable: bool) -> None:
+        """True (default): K RoPE and V^T come from the QKV projection's epilogue; False: a separate prep
+        kernel (same results; for checking the fused path)."""
+        check(load().mk_set_attn_prep_fused(self._h, int(enable)), "mk_set_attn_prep_fused")
+
     def set_max_chunk(self, seqs: int) -> None:
         """Cap the sequences per chunk of a large batch (0 = the default, include/mk.h); drops the cached
         per-shape buffers, whose workspace size depends on it."""

@@ -82,8 +82,9 @@ def test_packed_bytes_arithmetic():
     assert lib.mk_packed_bytes(ctypes.byref(cfg), b"int8d:qkv+gu|sq|lastbf16|fqkv|fmlp", ctypes.byref(n)) == 0
     Lm, H, I, D, qd = 23, 1536, 4608, 2560, 2048
     al = lambda v: (v + 255) // 256 * 256  # noqa: E731
-    exp = (al(Lm * D * H) + al(Lm * H * qd * 2) + al(Lm * 2 * I * H) + al(Lm * 2 * I * 4) + al(Lm * H * I * 2)
-           + al(D * H * 2) + al(H * qd * 2) + al(2 * I * H * 2) + al(H * I * 2))
+    # W_qkv + its column scales in the packed order, W_o, W_gu + scales, W_down, the last layer's bf16 weights
+    exp = (al(Lm * D * H) + al(Lm * D * 4) + al(Lm * H * qd * 2) + al(Lm * 2 * I * H) + al(Lm * 2 * I * 4)
+           + al(Lm * H * I * 2) + al(D * H * 2) + al(H * qd * 2) + al(2 * I * H * 2) + al(H * I * 2))
     assert n.value == exp
 
 

@@ -388,11 +388,53 @@ def test_forward_timed_matches_forward():
     t = m.forward_timed(ids.reshape(-1), 2, 512, logits=True)
     h2, lg2 = m.forward(ids.reshape(-1), 2, 512, logits=True, copy_out=False)   # buffers the timed run wrote
     L = cfg.num_layers - 1
-    assert t["attn"][1] == L and t["attn_prep"][1] == L and t["gemm_qkv"][1] == L and t["gemm_gu"][1] == L
+    # the QKV projection's epilogue does the attention prep: no prep launches
+    assert t["attn"][1] == L and t["attn_prep"][1] == 0 and t["gemm_qkv"][1] == L and t["gemm_gu"][1] == L
     assert t["embed"][1] == 1 and t["lm_head"][1] >= 1
     assert all(ms >= 0.0 for ms, _ in t.values()) and t["attn"][0] > 0.0
     assert torch.equal(h, h2) and torch.equal(lg, lg2)
+    m.set_attn_prep_fused(False)
+    assert m.forward_timed(ids.reshape(-1), 2, 512, logits=True)["attn_prep"][1] == L
     m.close()
+
+
+@pytest.mark.parametrize("name,quant,B,S", [
+    ("tiny", "int8d:qkv+gu|sq|lastbf16|fqkv|fmlp", 2, 512), ("tiny-hd96", "int8d:qkv+gu+o|sq|lastbf16", 3, 256),
+    ("tiny", "bf16", 2, 384), ("tiny-hd96", "fp8d|sq|lastbf16", 1, 640), ("tiny", "int8|sq|fqkv|fmlp", 2, 256)])
+def test_fused_attn_prep_equals_prep_kernel(name, quant, B, S):
+    """The QKV projection's routing epilogue (K RoPE'd into krope, V transposed into vt, pack.hip map 2
+    column order) gives the same model output, bitwise, as the projection followed by the separate prep
+    kernel, for every QKV epilogue (DQ_BF16, DQ2_BF16, BF16, fp8 DQ2_BF16) and both head dims."""
+    from minicpm5_mk.config import preset
+    from minicpm5_mk.synth import random_hf_state_dict, random_token_ids
+
+    dev = _dev()
+    cfg = preset(name)
+    sd = random_hf_state_dict(cfg)
+    m, _ = _build(cfg, quant, sd, 1024, dev)
+    ids = random_token_ids(B, S, seed=B + S).to(dev).reshape(-1)
+    h1, l1 = m.forward(ids, B, S, logits=True)
+    m.set_attn_prep_fused(False)
+    h0, l0 = m.forward(ids, B, S, logits=True)
+    assert torch.equal(h1, h0) and torch.equal(l1, l0)
+    m.close()
+
+
+def test_fused_attn_prep_full_size():
+    """Fused vs separate attention prep on the full MiniCPM5-1B at (2, 4096) and (1, 8192): bitwise equal."""
+    from minicpm5_mk.synth import random_token_ids
+
+    m = _full_model("1b")
+    dev = _dev()
+    for B, S in ((2, 4096), (1, 8192)):
+        ids = random_token_ids(B, S, seed=3).to(dev).reshape(-1)
+        print(f"[fused prep] 1b ({B}, {S})", flush=True)
+        h1, l1 = m.forward(ids, B, S, logits=True)
+        m.set_attn_prep_fused(False)
+        h0, l0 = m.forward(ids, B, S, logits=True)
+        m.set_attn_prep_fused(True)
+        assert torch.equal(h1, h0) and torch.equal(l1, l0)
+    m.release_buffers()
 
 
 @pytest.mark.parametrize("quant", ["int8d:qkv+gu|sq|lastbf16|fqkv|fmlp", "bf16"])
