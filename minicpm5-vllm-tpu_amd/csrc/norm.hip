@@ -1,6 +1,8 @@
 // HBM-bound row kernels: RMSNorm + dynamic int8 quantisation, bf16 RMSNorm, embedding gather and
 // small elementwise ops of the last-token layer (gfx950).  One wave per token row; rows are read
 // with 16-byte vector loads.
+#include <type_traits>
+
 #include "kernels.h"
 #include "mk_common.h"
 
@@ -50,7 +52,9 @@ __device__ inline void load8(const void* x, size_t off, float v[8]) {
 
 // Reference algebra: QuantArgs (kernels.h).  One wave per row; the row stays in registers (NC
 // 8-element chunks per lane, all loads issued before the first use) so the row costs one HBM round trip.
-template <bool F32, int NC, QKind KIND>
+// The per-element choices are compile-time (straight-line code): RN = a.recip for the dynamic modes
+// (q = u * (1/s) vs u / s) and a.norm for the static ones; HAS_A = (a.a != null).
+template <bool F32, int NC, QKind KIND, bool RN, bool HAS_A>
 __global__ __launch_bounds__(256) void rowquant_kernel(QuantArgs a) {
   constexpr bool DYN = KIND == QKind::I8D || KIND == QKind::F8D;
   constexpr bool FP8 = KIND == QKind::F8D || KIND == QKind::F8S;
@@ -65,10 +69,11 @@ __global__ __launch_bounds__(256) void rowquant_kernel(QuantArgs a) {
     const int c = lane + 64 * i;
     if (c < nc) load8<F32>(a.x, xo + 8 * c, v[i]);
   }
+  constexpr bool RECIP = DYN && RN, NORM_S = !DYN && RN;
   auto load_a = [&](int c, f32x4& a0, f32x4& a1) {
     a0 = f32x4{1.f, 1.f, 1.f, 1.f};
     a1 = a0;
-    if (a.a) {
+    if constexpr (HAS_A) {
       const f32x4* ap = reinterpret_cast<const f32x4*>(a.a + 8 * c);
       a0 = ap[0];
       a1 = ap[1];
@@ -85,7 +90,7 @@ __global__ __launch_bounds__(256) void rowquant_kernel(QuantArgs a) {
       for (int e = 0; e < 8; ++e) {
         ss += v[i][e] * v[i][e];
         if constexpr (DYN) {
-          v[i][e] = a.a ? v[i][e] * (e < 4 ? a0[e] : a1[e - 4]) : v[i][e];   // u = x * a
+          if constexpr (HAS_A) v[i][e] = v[i][e] * (e < 4 ? a0[e] : a1[e - 4]);   // u = x * a
           am = fmaxf(am, fabsf(v[i][e]));
         }
       }
@@ -105,13 +110,13 @@ __global__ __launch_bounds__(256) void rowquant_kernel(QuantArgs a) {
     float t[8];
     if constexpr (DYN) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) t[e] = a.recip ? v[i][e] * inv : v[i][e] / s_u;
+      for (int e = 0; e < 8; ++e) t[e] = RECIP ? v[i][e] * inv : v[i][e] / s_u;
     } else {
       f32x4 a0, a1;
       load_a(c, a0, a1);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float xn = a.norm ? bf2f(f2bf(v[i][e] * rstd)) : v[i][e];
+        const float xn = NORM_S ? bf2f(f2bf(v[i][e] * rstd)) : v[i][e];
         t[e] = xn * (e < 4 ? a0[e] : a1[e - 4]);
       }
     }
@@ -227,27 +232,46 @@ int launch_rowquant(const QuantArgs& a, hipStream_t st) {
   const dim3 grid((a.T + 3) / 4);
   const int nc = (a.H / 8 + 63) / 64;   // 8-element chunks per lane
   MK_REQUIRE(!a.x_f32 || a.kind == QKind::I8D, "rowquant: f32 input is only taken by the int8d mode");
-#define MK_RQK(NC, K)                                                                                   \
-  if (a.x_f32) hipLaunchKernelGGL((rowquant_kernel<true, NC, K>), grid, dim3(256), 0, st, a);        \
-  else hipLaunchKernelGGL((rowquant_kernel<false, NC, K>), grid, dim3(256), 0, st, a);
-#define MK_RQ(NC)                                                                          \
-  switch (a.kind) {                                                                        \
-    case QKind::I8D: MK_RQK(NC, QKind::I8D) break;                                         \
-    case QKind::F8D: hipLaunchKernelGGL((rowquant_kernel<false, NC, QKind::F8D>), grid, dim3(256), 0, st, a); break; \
-    case QKind::I8S: hipLaunchKernelGGL((rowquant_kernel<false, NC, QKind::I8S>), grid, dim3(256), 0, st, a); break; \
-    case QKind::F8S: hipLaunchKernelGGL((rowquant_kernel<false, NC, QKind::F8S>), grid, dim3(256), 0, st, a); break; \
-  }
-  if (nc <= 4) {
-    MK_RQ(4)
-  } else if (nc <= 8) {
-    MK_RQ(8)
-  } else if (nc <= 12) {
-    MK_RQ(12)
-  } else {
-    MK_RQ(16)
-  }
-#undef MK_RQ
-#undef MK_RQK
+  const bool dyn = a.kind == QKind::I8D || a.kind == QKind::F8D;
+  const bool rn = dyn ? a.recip : a.norm;
+  auto go = [&](auto ncv, auto kv) {
+    constexpr int NC = decltype(ncv)::value;
+    constexpr QKind K = decltype(kv)::value;
+    auto go2 = [&](auto f32v, auto rnv, auto hav) {
+      hipLaunchKernelGGL((rowquant_kernel<decltype(f32v)::value, NC, K, decltype(rnv)::value, decltype(hav)::value>),
+                         grid, dim3(256), 0, st, a);
+    };
+    using T_ = std::true_type;
+    using F_ = std::false_type;
+    auto go1 = [&](auto f32v) {
+      if (rn) {
+        if (a.a) go2(f32v, T_{}, T_{});
+        else go2(f32v, T_{}, F_{});
+      } else {
+        if (a.a) go2(f32v, F_{}, T_{});
+        else go2(f32v, F_{}, F_{});
+      }
+    };
+    if constexpr (K == QKind::I8D) {
+      if (a.x_f32) go1(T_{});
+      else go1(F_{});
+    } else {
+      go1(F_{});
+    }
+  };
+  auto kinds = [&](auto ncv) {
+    switch (a.kind) {
+      case QKind::I8D: go(ncv, std::integral_constant<QKind, QKind::I8D>{}); break;
+      case QKind::F8D: go(ncv, std::integral_constant<QKind, QKind::F8D>{}); break;
+      case QKind::I8S: go(ncv, std::integral_constant<QKind, QKind::I8S>{}); break;
+      case QKind::F8S: go(ncv, std::integral_constant<QKind, QKind::F8S>{}); break;
+    }
+  };
+  if (nc <= 3) kinds(std::integral_constant<int, 3>{});
+  else if (nc <= 4) kinds(std::integral_constant<int, 4>{});
+  else if (nc <= 8) kinds(std::integral_constant<int, 8>{});
+  else if (nc <= 12) kinds(std::integral_constant<int, 12>{});
+  else kinds(std::integral_constant<int, 16>{});
   MK_HIP_CHECK(hipGetLastError());
   return MK_OK;
 }
