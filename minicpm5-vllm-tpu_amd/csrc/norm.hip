@@ -63,36 +63,51 @@ __global__ __launch_bounds__(256) void rowquant_kernel(QuantArgs a) {
   if (row >= a.T) return;
   const int nc = a.H / 8;
   const size_t xo = (size_t)row * a.ldx;
+  constexpr bool RECIP = DYN && RN, NORM_S = !DYN && RN;
+  // Every load is issued before the first use: chunk indices are clamped in bounds (no branch around a
+  // load, which would make each one wait for the previous), and the chunks past the row end are zeroed
+  // on their raw bits, so they add nothing to the sum of squares or the amax.
   float v[NC][8];
+  f32x4 av[NC][2];   // per-channel factors a (ones when absent)
 #pragma unroll
   for (int i = 0; i < NC; ++i) {
-    const int c = lane + 64 * i;
-    if (c < nc) load8<F32>(a.x, xo + 8 * c, v[i]);
-  }
-  constexpr bool RECIP = DYN && RN, NORM_S = !DYN && RN;
-  auto load_a = [&](int c, f32x4& a0, f32x4& a1) {
-    a0 = f32x4{1.f, 1.f, 1.f, 1.f};
-    a1 = a0;
+    const bool valid = lane + 64 * i < nc;
+    const int c = min(lane + 64 * i, nc - 1);
+    if constexpr (F32) {
+      const f32x4* p = reinterpret_cast<const f32x4*>(static_cast<const float*>(a.x) + xo + 8 * c);
+      const f32x4 x0 = p[0], x1 = p[1];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[i][e] = valid ? x0[e] : 0.f;
+        v[i][4 + e] = valid ? x1[e] : 0.f;
+      }
+    } else {
+      u32x4 r = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.x) + xo + 8 * c);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        r[e] = valid ? r[e] : 0u;
+        v[i][2 * e] = bf_lo(r[e]);
+        v[i][2 * e + 1] = bf_hi(r[e]);
+      }
+    }
     if constexpr (HAS_A) {
       const f32x4* ap = reinterpret_cast<const f32x4*>(a.a + 8 * c);
-      a0 = ap[0];
-      a1 = ap[1];
+      av[i][0] = ap[0];
+      av[i][1] = ap[1];
+    } else {
+      av[i][0] = f32x4{1.f, 1.f, 1.f, 1.f};
+      av[i][1] = av[i][0];
     }
-  };
+  }
   float ss = 0.f, am = 0.f;
 #pragma unroll
   for (int i = 0; i < NC; ++i) {
-    const int c = lane + 64 * i;
-    if (c < nc) {
-      f32x4 a0, a1;
-      if constexpr (DYN) load_a(c, a0, a1);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        ss += v[i][e] * v[i][e];
-        if constexpr (DYN) {
-          if constexpr (HAS_A) v[i][e] = v[i][e] * (e < 4 ? a0[e] : a1[e - 4]);   // u = x * a
-          am = fmaxf(am, fabsf(v[i][e]));
-        }
+    for (int e = 0; e < 8; ++e) {
+      ss += v[i][e] * v[i][e];
+      if constexpr (DYN) {
+        if constexpr (HAS_A) v[i][e] = v[i][e] * (e < 4 ? av[i][0][e] : av[i][1][e - 4]);   // u = x * a
+        am = fmaxf(am, fabsf(v[i][e]));
       }
     }
   }
@@ -110,14 +125,22 @@ __global__ __launch_bounds__(256) void rowquant_kernel(QuantArgs a) {
     float t[8];
     if constexpr (DYN) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) t[e] = RECIP ? v[i][e] * inv : v[i][e] / s_u;
+      for (int e = 0; e < 8; ++e) {
+        if constexpr (RECIP) {
+          t[e] = v[i][e] * inv;
+        } else {
+          // u / s correctly rounded from inv = RN(1 / s) (an IEEE division, once per row) and two FMAs
+          // per element (Markstein: q0 = RN(u inv) is faithful, r = u - s q0 is exact, RN(q0 + r inv) =
+          // RN(u / s)); |u / s| <= 127, and a quotient small enough for r to lose bits rounds to 0
+          const float q0 = v[i][e] * inv;
+          t[e] = __builtin_fmaf(__builtin_fmaf(-q0, s_u, v[i][e]), inv, q0);
+        }
+      }
     } else {
-      f32x4 a0, a1;
-      load_a(c, a0, a1);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float xn = NORM_S ? bf2f(f2bf(v[i][e] * rstd)) : v[i][e];
-        t[e] = xn * (e < 4 ? a0[e] : a1[e - 4]);
+        t[e] = xn * (e < 4 ? av[i][0][e] : av[i][1][e - 4]);
       }
     }
     uint32_t w0 = 0, w1 = 0;
