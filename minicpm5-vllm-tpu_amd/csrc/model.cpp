@@ -415,7 +415,10 @@ int launch_forward(const Fwd& f, hipStream_t st) {
     g.out = qkv;
     g.ldo = D;
     g.B = pb + m.P.wqkv + (size_t)l * D * H * e0;
-    if (m.fuse_prep) {   // the QKV epilogue writes the attention's RoPE'd K and V^T (and empties its queues)
+    // the QKV epilogue writes the attention's RoPE'd K and V^T (and empties its queues) when the K and V
+    // column blocks start at multiples of its 64-column passes (n_kv even at hd 96); else the prep kernel
+    const bool fuse = m.fuse_prep && qd % 64 == 0 && (qd + kvd) % 64 == 0;
+    if (fuse) {
       g.krope = aa.krope;
       g.vt = aa.vt;
       g.cos = cosr;
@@ -448,7 +451,7 @@ int launch_forward(const Fwd& f, hipStream_t st) {
     }
     kind = MK_KERNEL_GEMM_QKV;
     MK_RUN(launch_gemm(g, st));
-    if (!m.fuse_prep) {
+    if (!fuse) {
       kind = MK_KERNEL_ATTN_PREP;
       MK_RUN(launch_attn_stages(aa, st, 1));
     }

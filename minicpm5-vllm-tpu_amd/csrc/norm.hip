@@ -175,7 +175,8 @@ __global__ __launch_bounds__(256) void rmsnorm_bf16_kernel(const uint16_t* __res
   const int nc = H / 8;
   const uint16_t* xr = x + (size_t)row * ldx;
   float ss = 0.f;
-  for (int c = lane; c < nc; c += 64) {
+#pragma unroll 4
+  for (int c = lane; c < nc; c += 64) {   // unrolled: the loads of several chunks in flight at once
     float v[8];
     load8<false>(xr, 8 * c, v);
 #pragma unroll
@@ -184,6 +185,7 @@ __global__ __launch_bounds__(256) void rmsnorm_bf16_kernel(const uint16_t* __res
   ss = wave_sum(ss);
   const float rstd = 1.f / sqrtf(ss / (float)H + eps);
   uint16_t* orow = out + (size_t)row * ldo;
+#pragma unroll 4
   for (int c = lane; c < nc; c += 64) {
     float v[8];
     load8<false>(xr, 8 * c, v);
@@ -210,7 +212,8 @@ __global__ __launch_bounds__(256) void embed_kernel(const int32_t* __restrict__ 
   id = id < 0 ? 0 : (id >= V ? V - 1 : id);   // memory safety: out-of-range ids are clamped
   const u32x4* src = reinterpret_cast<const u32x4*>(embed + (size_t)id * H);
   u32x4* dst = reinterpret_cast<u32x4*>(x + (size_t)row * H);
-  for (int c = lane; c < H / 8; c += 64) dst[c] = src[c];
+#pragma unroll 4
+  for (int c = lane; c < H / 8; c += 64) dst[c] = src[c];   // unrolled: several row chunks in flight
 }
 
 __global__ void gather_last_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ rows, int S,

@@ -85,6 +85,35 @@ def test_tiny_vs_emulator(name, quant):
     m.close()
 
 
+def test_one_kv_head_hd96_vs_emulator():
+    """8 query heads over 1 kv head at head_dim 96: the K and V column blocks of the QKV projection do
+    not start at multiples of 64 (768 + 96), so the attention's RoPE'd K / V^T come from the prep kernel
+    instead of the projection's epilogue; the model still matches the emulator like the other tiny
+    configurations, and switching the fused prep on or off changes nothing."""
+    import dataclasses
+
+    from minicpm5_mk.config import preset
+    from minicpm5_mk.synth import random_hf_state_dict, random_token_ids
+    from oracle import emulate
+
+    dev = _dev()
+    cfg = dataclasses.replace(preset("tiny-hd96"), n_q=8, n_kv=1, name="tiny-hd96-kv1")
+    quant = "int8d:qkv+gu|sq|lastbf16|fqkv|fmlp"
+    sd = random_hf_state_dict(cfg)
+    ids = random_token_ids(2, 256, seed=9)
+    m, w = _build(cfg, quant, sd, 1024, dev)
+    hid, lg = m.forward(ids.reshape(-1).to(dev), 2, 256, logits=True)
+    m.set_attn_prep_fused(False)
+    hid0, lg0 = m.forward(ids.reshape(-1).to(dev), 2, 256, logits=True)
+    assert torch.equal(hid, hid0) and torch.equal(lg, lg0)
+    _, lg_ref = emulate.mk_forward(ids, w, sd["model.embed_tokens.weight"], sd["model.norm.weight"], cfg, quant,
+                                   sd["lm_head.weight"])
+    err = (lg.cpu() - lg_ref).abs()
+    print(f"[model] tiny-hd96-kv1 logits max {err.max():.4g} mean {err.mean():.4g}", flush=True)
+    assert err.max() <= 0.05 and err.mean() <= 1e-2
+    m.close()
+
+
 @pytest.mark.parametrize("name,B,S", [("tiny", 3, 128), ("tiny-hd96", 2, 384), ("tiny", 1, 896)])
 def test_short_seq_vs_emulator(name, B, S):
     """Lengths the reference serves below 1024 (multiples of 128, model.py:131-136): the last chunk of
