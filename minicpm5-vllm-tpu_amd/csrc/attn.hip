@@ -748,7 +748,8 @@ __global__ __launch_bounds__(MERGE_T) void last_attn_merge_kernel(LastAttnArgs a
   if (tid < NG * HD) {
     const int d = tid % HD, g = tid / HD;
     float o = 0.f;
-    for (int c = g; c < nchunk; c += NG) o += pp[(size_t)c * (HD + 2) + 2 + d] * ec[c];
+#pragma unroll 8
+    for (int c = g; c < nchunk; c += NG) o += pp[(size_t)c * (HD + 2) + 2 + d] * ec[c];   // loads in flight together
     osum[g][d] = o;
   }
   __syncthreads();

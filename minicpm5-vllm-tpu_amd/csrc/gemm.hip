@@ -759,7 +759,8 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(GemmArgs g, int spli
   if (i >= (size_t)g.M * g.N) return;
   const int m = (int)(i / g.N), n = (int)(i % g.N);
   float v = 0.f;
-  for (int s = 0; s < splits; ++s) v += part[((size_t)s * g.M + m) * g.N + n];
+#pragma unroll 4
+  for (int s = 0; s < splits; ++s) v += part[((size_t)s * g.M + m) * g.N + n];   // in split order
   epi_store<EPI>(g, m, n, v);
 }
 

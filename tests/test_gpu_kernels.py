@@ -19,6 +19,7 @@
 """
 import math
 
+import numpy as np
 import pytest
 import torch
 
@@ -95,7 +96,8 @@ def test_attention_batch_invariant(B, S, hd):
 
 
 @pytest.mark.parametrize("T,H,norm,recip,f32", [(300, 1536, True, True, False), (64, 2048, False, False, False),
-                                                (129, 4608, False, True, True), (8192, 1536, True, True, False)])
+                                                (129, 4608, False, True, True), (8192, 1536, True, True, False),
+                                                (77, 256, True, True, False), (5, 1280, True, False, True)])
 def test_row_quant_bitexact(T, H, norm, recip, f32):
     from minicpm5_mk import ops
     from oracle import emulate
@@ -113,6 +115,50 @@ def test_row_quant_bitexact(T, H, norm, recip, f32):
         torch.testing.assert_close(sx.cpu(), sxr, rtol=4e-7, atol=0)
     else:
         assert torch.equal(sx.cpu(), sxr)
+
+
+def _rowquant_tree_sx(x: np.ndarray, a: np.ndarray, eps: float) -> np.ndarray:
+    """The fused prologue's per-token scale sx = max(amax(x a) / 127, 1e-6) * rsqrt(mean(x^2) + eps) with the
+    sum of squares added in the kernel's order: lane L (of 64) sums chunks L + 64 i (8 elements each) with
+    FMAs, then the DPP tree (partners L^1, L^2, the 8-lane mirror, the 16-lane mirror) and
+    (L0 + L16) + (L32 + L48).  Float32 throughout; a bf16 square is exact in float64, so
+    f32(f64(v)^2 + f64(s)) is the FMA."""
+    f32 = np.float32
+    T, H = x.shape
+    nc = H // 8
+    out = np.empty(T, dtype=f32)
+    for t in range(T):
+        lanes = np.zeros(64, dtype=f32)
+        for L in range(64):
+            s = f32(0.0)
+            for c in range(L, nc, 64):
+                for e in range(8):
+                    v = np.float64(x[t, 8 * c + e])
+                    s = f32(v * v + np.float64(s))
+            lanes[L] = s
+        for part in (lambda l: l ^ 1, lambda l: l ^ 2, lambda l: (l & ~7) | (7 - (l & 7)),
+                     lambda l: (l & ~15) | (15 - (l & 15))):
+            lanes = np.array([f32(lanes[l] + lanes[part(l)]) for l in range(64)], dtype=f32)
+        ss = f32(f32(lanes[0] + lanes[16]) + f32(lanes[32] + lanes[48]))
+        rstd = f32(1.0) / np.sqrt(f32(ss / f32(H)) + f32(eps), dtype=f32)
+        am = np.max(np.abs(x[t].astype(f32) * a.astype(f32)))
+        out[t] = f32(max(f32(am * f32(1.0 / 127.0)), f32(1e-6)) * rstd)
+    return out
+
+
+@pytest.mark.parametrize("T,H", [(9, 1536), (7, 2048), (3, 1280)])
+def test_row_quant_scale_tree_bitexact(T, H):
+    """sx bit for bit against a restatement of the kernel's summation order (per-lane FMAs over chunks
+    L + 64 i, then the DPP tree), rows with 2, 3 and 4 chunks per lane (the last one partly past the row)."""
+    from minicpm5_mk import ops
+
+    dev = _dev()
+    g = torch.Generator().manual_seed(T * H)
+    x = (torch.randn(T, H, generator=g) * 3).to(BF16)
+    a = torch.rand(H, generator=g) + 0.5
+    _, sx = ops.row_quant(x.to(dev), a.to(dev), 1e-6, True, True)
+    ref = _rowquant_tree_sx(x.float().numpy(), a.numpy(), 1e-6)
+    assert np.array_equal(sx.cpu().numpy().view(np.uint32), ref.view(np.uint32))
 
 
 @pytest.mark.parametrize("M,N,K", [(256, 128, 64), (300, 200, 1536), (8192, 1920, 1536), (1000, 1536, 4608)])
