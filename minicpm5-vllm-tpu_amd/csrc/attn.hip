@@ -26,6 +26,14 @@ namespace mk {
 
 namespace {
 
+typedef uint64_t u64x8 __attribute__((ext_vector_type(8)));
+// a 64-bit register-pair copy in one instruction (the compiler splits a 64-bit splat into 32-bit moves)
+__device__ inline uint64_t mov64(uint64_t s) {
+  uint64_t d;
+  asm volatile("v_mov_b64 %0, %1" : "=v"(d) : "v"(s));
+  return d;
+}
+
 constexpr int QT = 32;   // tokens per q tile (MFMA column block)
 constexpr int KT = 64;   // keys per K/V tile
 constexpr int G = 8;     // q heads per kv head == waves per workgroup
@@ -173,7 +181,8 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_fwd_kernel(
   char* const vring = smem + L::NK * L::KBYTES;
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, w = tid >> 6;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index, kept in an SGPR
   const int col = lane & 31, half = lane >> 5;
   // Work items are (kv head, group of GW of its G q heads, sequence, 32-token q tile); a wave computes
   // one q head.  Which workgroup computes an item, and how many heads it shares K / V with (GW), does
@@ -218,25 +227,27 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_fwd_kernel(
   constexpr int VIN = (HD * VRC + 63) / 64;          // per V^T tile (the last one partial at hd 96)
   constexpr int KIW = (KIN + GW - 1) / GW, VIW = (VIN + GW - 1) / GW;   // per wave, at most
   static_assert(KT * KRC % 64 == 0, "K image is whole instructions");
-  uint32_t koff[KIW], voff[VIW];                     // element offset of this lane's chunk in a tile
+  // byte offset of this lane's chunk within a tile; the tile's own offset goes in the instruction's
+  // scalar offset, so a copy costs no VALU work
+  uint32_t koff[KIW], voff[VIW];
 #pragma unroll
   for (int i = 0; i < KIW; ++i) {
     const int ch = 64 * (w + GW * i) + lane;
     const int row = min(ch / KRC, KT - 1), pos = ch % KRC;
-    koff[i] = row * HD + (pos < HD / 8 ? pos : 0) * 8;
+    koff[i] = 2u * (row * HD + (pos < HD / 8 ? pos : 0) * 8);
   }
 #pragma unroll
   for (int i = 0; i < VIW; ++i) {
     const int ch = 64 * (w + GW * i) + lane;
     const int d = min(ch / VRC, HD - 1), pos = ch % VRC;
-    voff[i] = d * S + (pos < KT / 8 ? pos : 0) * 8;
+    voff[i] = 2u * (d * S + (pos < KT / 8 ? pos : 0) * 8);
   }
   auto aload_k = [&](int kt, int slot) {
     char* dst = kring + slot * L::KBYTES;
 #pragma unroll
     for (int i = 0; i < KIW; ++i) {
       const int ins = w + GW * i;
-      if (KIN % GW == 0 || ins < KIN) copy16_to_lds(krs, 2u * (kt * KT * HD + koff[i]), dst + 1024 * ins);
+      if (KIN % GW == 0 || ins < KIN) copy16_to_lds(krs, koff[i], 2u * (kt * KT * HD), dst + 1024 * ins);
     }
   };
   auto aload_v = [&](int kt, int slot) {
@@ -246,7 +257,7 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_fwd_kernel(
       const int ins = w + GW * i;
       if (VIN % GW == 0 || ins < VIN) {
         if (HD * VRC % 64 == 0 || 64 * ins + lane < HD * VRC)
-          copy16_to_lds(vrs, 2u * (kt * KT + voff[i]), dst + 1024 * ins);
+          copy16_to_lds(vrs, voff[i], 2u * (kt * KT), dst + 1024 * ins);
       }
     }
   };
@@ -267,7 +278,7 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_fwd_kernel(
         *item_s = it;
       }
       __syncthreads();
-      const int item = *item_s;
+      const int item = __builtin_amdgcn_readfirstlane(*item_s);
       if (item < 0) break;
       kv = item / nper;
       const int v = item % nper;                     // longest tiles first
@@ -439,12 +450,17 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_fwd_kernel(
         pb[c][s2][e] = pack_bf2(p0, p1);
         psum = dot2_bf16_sum(pb[c][s2][e], psum);
       };
+      float mx = -INFINITY;
       {
-        f32x16 nm;
+        // the QK MFMAs accumulate onto -m: S - m with no subtraction per score.  -m is built in all 16
+        // accumulator slots as 8 register pairs (9 instructions, not 16)
+        u64x8 nm;
+        const uint64_t b = __float_as_uint(-m);
+        nm[0] = (b << 32) | b;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) nm[r] = -m;
-        sn[0] = nm;   // the QK MFMAs accumulate onto -m: S - m with no subtraction per score
-        sn[1] = nm;
+        for (int i = 1; i < 8; ++i) nm[i] = mov64(nm[0]);
+        sn[0] = __builtin_bit_cast(f32x16, nm);
+        sn[1] = sn[0];
       }
 #pragma unroll
       for (int j = 0; j < PF; ++j) kr[j] = kread(j);
@@ -472,7 +488,6 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_fwd_kernel(
         return *reinterpret_cast<const u32x4*>(vsl + (dt * 32 + col) * L::VROW + (32 * c + 16 * s2 + 8 * half) * 2);
       };
       u32x4 vr[NPV];
-      float mx = -INFINITY;
 #pragma unroll
       for (int j = 0; j < PF; ++j) vr[j] = vread(j);
 #pragma unroll

@@ -124,6 +124,12 @@ __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t by
 __device__ inline void copy16_to_lds(__amdgpu_buffer_rsrc_t r, uint32_t off, char* dst) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)dst, 16, off, 0, 0, 0);
 }
+// The same with the offset split into a per-lane part `voff` and a wave-uniform part `soff` (the
+// instruction's SGPR offset, added with no VALU work).  The range check covers `voff` alone, so
+// callers keep soff + voff inside the buffer themselves.
+__device__ inline void copy16_to_lds(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, char* dst) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)dst, 16, voff, soff, 0, 0);
+}
 
 // acc + lo(w) + hi(w) for a packed bf16 pair (v_dot2_f32_bf16 with (1, 1))
 __device__ inline float dot2_bf16_sum(uint32_t w, float acc) {
