@@ -646,41 +646,70 @@ __global__ __launch_bounds__(256) void last_attn_part_kernel(LastAttnArgs a) {
   const int nchunk = a.S / LCH;
   const int kvdim = a.n_kv * HD;
   const size_t pos_last = (size_t)(a.S - 1) * HD;
-  for (int i = tid; i < G * HD; i += 256) {
-    const int h = i / HD, d = i % HD;
-    const uint16_t* q = a.q + ((size_t)b * a.n_q + kv * G + h) * HD;
-    const float x = bf2f(q[d]);
-    const float y = d < H2 ? -bf2f(q[d + H2]) : bf2f(q[d - H2]);
-    qs[h][d] = bf2f(f2bf(x * bf2f(a.cos[pos_last + d]) + y * bf2f(a.sin[pos_last + d])));
-  }
-  // K: 16-byte chunks c (8 dims) and their rotate-half partners c + HD / 16, RoPE'd at the key's position
   const size_t row0 = (size_t)b * a.S + (size_t)chunk * LCH;
-  for (int i = tid; i < LCH * (HD / 16); i += 256) {
-    const int key = i / (HD / 16), c = i % (HD / 16);
-    const uint16_t* krow = a.kv + (row0 + key) * (2 * kvdim) + kv * HD;
-    const u32x4 lo = *reinterpret_cast<const u32x4*>(krow + 8 * c);
-    const u32x4 hi = *reinterpret_cast<const u32x4*>(krow + H2 + 8 * c);
-    const size_t tb = (size_t)(chunk * LCH + key) * HD;
-    const u32x4 cl = *reinterpret_cast<const u32x4*>(a.cos + tb + 8 * c);
-    const u32x4 ch = *reinterpret_cast<const u32x4*>(a.cos + tb + H2 + 8 * c);
-    const u32x4 sl = *reinterpret_cast<const u32x4*>(a.sin + tb + 8 * c);
-    const u32x4 sh = *reinterpret_cast<const u32x4*>(a.sin + tb + H2 + 8 * c);
+  // Every global load of the workgroup is issued first (one memory latency), then q and K are
+  // RoPE'd and q, K, V stored to LDS.  q: element i = h HD + d; K: 16-byte chunk c (8 dims) of a
+  // key and its rotate-half partner c + HD / 16, RoPE'd at the key's position; V: 16-byte chunks.
+  constexpr int NQE = G * HD / 256, NKC = LCH * (HD / 16), NKI = (NKC + 255) / 256, NVI = LCH * (HD / 8) / 256;
+  static_assert(G * HD % 256 == 0 && LCH * (HD / 8) % 256 == 0, "q and V split evenly over the threads");
+  uint16_t qx[NQE], qy[NQE], qc[NQE], qsn[NQE];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float x1 = e & 1 ? bf_hi(lo[e / 2]) : bf_lo(lo[e / 2]);
-      const float x2 = e & 1 ? bf_hi(hi[e / 2]) : bf_lo(hi[e / 2]);
-      const float c1 = e & 1 ? bf_hi(cl[e / 2]) : bf_lo(cl[e / 2]);
-      const float c2 = e & 1 ? bf_hi(ch[e / 2]) : bf_lo(ch[e / 2]);
-      const float s1 = e & 1 ? bf_hi(sl[e / 2]) : bf_lo(sl[e / 2]);
-      const float s2 = e & 1 ? bf_hi(sh[e / 2]) : bf_lo(sh[e / 2]);
-      ks[key][8 * c + e] = bf2f(f2bf(x1 * c1 - x2 * s1));
-      ks[key][H2 + 8 * c + e] = bf2f(f2bf(x2 * c2 + x1 * s2));
+  for (int j = 0; j < NQE; ++j) {
+    const int i = tid + 256 * j, h = i / HD, d = i % HD;
+    const uint16_t* q = a.q + ((size_t)b * a.n_q + kv * G + h) * HD;
+    qx[j] = q[d];
+    qy[j] = q[d < H2 ? d + H2 : d - H2];
+    qc[j] = a.cos[pos_last + d];
+    qsn[j] = a.sin[pos_last + d];
+  }
+  u32x4 klo[NKI], khi[NKI], kcl[NKI], kch[NKI], ksl[NKI], ksh[NKI];
+#pragma unroll
+  for (int j = 0; j < NKI; ++j) {
+    const int i = min(tid + 256 * j, NKC - 1), key = i / (HD / 16), c = i % (HD / 16);
+    const uint16_t* krow = a.kv + (row0 + key) * (2 * kvdim) + kv * HD;
+    const size_t tb = (size_t)(chunk * LCH + key) * HD;
+    klo[j] = *reinterpret_cast<const u32x4*>(krow + 8 * c);
+    khi[j] = *reinterpret_cast<const u32x4*>(krow + H2 + 8 * c);
+    kcl[j] = *reinterpret_cast<const u32x4*>(a.cos + tb + 8 * c);
+    kch[j] = *reinterpret_cast<const u32x4*>(a.cos + tb + H2 + 8 * c);
+    ksl[j] = *reinterpret_cast<const u32x4*>(a.sin + tb + 8 * c);
+    ksh[j] = *reinterpret_cast<const u32x4*>(a.sin + tb + H2 + 8 * c);
+  }
+  u32x4 vv[NVI];
+#pragma unroll
+  for (int j = 0; j < NVI; ++j) {
+    const int i = tid + 256 * j, key = i / (HD / 8), c = i % (HD / 8);
+    vv[j] = *reinterpret_cast<const u32x4*>(a.kv + (row0 + key) * (2 * kvdim) + kvdim + kv * HD + 8 * c);
+  }
+#pragma unroll
+  for (int j = 0; j < NQE; ++j) {
+    const int i = tid + 256 * j, h = i / HD, d = i % HD;
+    const float x = bf2f(qx[j]);
+    const float y = d < H2 ? -bf2f(qy[j]) : bf2f(qy[j]);
+    qs[h][d] = bf2f(f2bf(x * bf2f(qc[j]) + y * bf2f(qsn[j])));
+  }
+#pragma unroll
+  for (int j = 0; j < NKI; ++j) {
+    const int i = tid + 256 * j;
+    if (NKC % 256 == 0 || i < NKC) {
+      const int key = i / (HD / 16), c = i % (HD / 16);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float x1 = e & 1 ? bf_hi(klo[j][e / 2]) : bf_lo(klo[j][e / 2]);
+        const float x2 = e & 1 ? bf_hi(khi[j][e / 2]) : bf_lo(khi[j][e / 2]);
+        const float c1 = e & 1 ? bf_hi(kcl[j][e / 2]) : bf_lo(kcl[j][e / 2]);
+        const float c2 = e & 1 ? bf_hi(kch[j][e / 2]) : bf_lo(kch[j][e / 2]);
+        const float s1 = e & 1 ? bf_hi(ksl[j][e / 2]) : bf_lo(ksl[j][e / 2]);
+        const float s2 = e & 1 ? bf_hi(ksh[j][e / 2]) : bf_lo(ksh[j][e / 2]);
+        ks[key][8 * c + e] = bf2f(f2bf(x1 * c1 - x2 * s1));
+        ks[key][H2 + 8 * c + e] = bf2f(f2bf(x2 * c2 + x1 * s2));
+      }
     }
   }
-  for (int i = tid; i < LCH * (HD / 8); i += 256) {
-    const int key = i / (HD / 8), c = i % (HD / 8);
-    *reinterpret_cast<u32x4*>(&vs[key][8 * c]) =
-        *reinterpret_cast<const u32x4*>(a.kv + (row0 + key) * (2 * kvdim) + kvdim + kv * HD + 8 * c);
+#pragma unroll
+  for (int j = 0; j < NVI; ++j) {
+    const int i = tid + 256 * j, key = i / (HD / 8), c = i % (HD / 8);
+    *reinterpret_cast<u32x4*>(&vs[key][8 * c]) = vv[j];
   }
   __syncthreads();
   // scores of key `lane` for heads 2w, 2w + 1; max and sum over the chunk's keys within the wave
@@ -723,18 +752,29 @@ __global__ __launch_bounds__(256) void last_attn_part_kernel(LastAttnArgs a) {
 }
 
 // Merge of the chunk partials of one (head, sequence): M = max m_c, e_c = exp(m_c - M),
-// l = sum l_c e_c, o = sum o_c e_c; out = bf16(o / l).  256 threads: the chunks are split over
-// the threads in a fixed pattern and the partial sums combined in a fixed order.
-constexpr int MERGE_T = 256, MAX_CHUNKS = 2048;
+// l = sum l_c e_c, o = sum o_c e_c; out = bf16(o / l).  1024 threads: thread (g, d) sums o over the
+// chunks c = g, g + NG, ... (NG = 1024 / hd groups) and the group sums are added in group order, so
+// the result is fixed; its first OU partial values are loaded before the max / sum reductions that
+// their weights need, so the whole merge costs about one memory latency.
+constexpr int MERGE_T = 1024, MAX_CHUNKS = 2048, MERGE_OU = 16;
 
 template <int HD>
 __global__ __launch_bounds__(MERGE_T) void last_attn_merge_kernel(LastAttnArgs a) {
+  constexpr int NG = MERGE_T / HD;
   __shared__ float ec[MAX_CHUNKS];
   __shared__ float red[MERGE_T / 64];
-  __shared__ float osum[MERGE_T / HD + 1][HD];
+  __shared__ float osum[NG][HD];
   const int head = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int nchunk = a.S / LCH;
   const float* pp = a.part + ((size_t)b * a.n_q + head) * nchunk * (HD + 2);
+  const bool ot = tid < NG * HD;
+  const int d = tid % HD, g = tid / HD;
+  float ov[MERGE_OU];
+#pragma unroll
+  for (int u = 0; u < MERGE_OU; ++u) {
+    const int c = g + NG * u;
+    ov[u] = ot && c < nchunk ? pp[(size_t)c * (HD + 2) + 2 + d] : 0.f;
+  }
   float mx = -INFINITY;
   for (int c = tid; c < nchunk; c += MERGE_T) mx = fmaxf(mx, pp[(size_t)c * (HD + 2)]);
 #pragma unroll
@@ -758,20 +798,22 @@ __global__ __launch_bounds__(MERGE_T) void last_attn_merge_kernel(LastAttnArgs a
   float L = 0.f;
 #pragma unroll
   for (int i = 0; i < MERGE_T / 64; ++i) L += red[i];
-  // o: thread = (d, group g of chunks c = g, g + NG, ...), NG = threads per d
-  constexpr int NG = MERGE_T / HD;
-  if (tid < NG * HD) {
-    const int d = tid % HD, g = tid / HD;
+  if (ot) {
     float o = 0.f;
+#pragma unroll
+    for (int u = 0; u < MERGE_OU; ++u) {
+      const int c = g + NG * u;
+      if (c < nchunk) o += ov[u] * ec[c];
+    }
 #pragma unroll 8
-    for (int c = g; c < nchunk; c += NG) o += pp[(size_t)c * (HD + 2) + 2 + d] * ec[c];   // loads in flight together
+    for (int c = g + NG * MERGE_OU; c < nchunk; c += NG) o += pp[(size_t)c * (HD + 2) + 2 + d] * ec[c];
     osum[g][d] = o;
   }
   __syncthreads();
   if (tid < HD) {
     float o = 0.f;
 #pragma unroll
-    for (int g = 0; g < NG; ++g) o += osum[g][tid];
+    for (int i = 0; i < NG; ++i) o += osum[i][tid];
     a.out[((size_t)b * a.n_q + head) * HD + tid] = f2bf(o / L);
   }
 }
