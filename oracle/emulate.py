@@ -20,6 +20,8 @@ stated), with the reference's rounding points:
                    separately; `ref_numerics=True` reproduces those two TPU-specific roundings.
   attention_fp32   the FP32 reference attention of the attention-kernel benchmark (RoPE in f32 on
                    the bf16 inputs, f32 softmax).
+  attention_small  the reference's S <= 1024 kernel (mk_jax.py:58-175): bf16 RoPE products, exact
+                   row max, f32 exp and sum, P normalised to bf16 before the PV product.
   last_layer_step  mk_jax.py:492-520
   mk_forward       mk_jax.py:527-569, 608-665 (+ the inherited LM head in f32)
 
@@ -238,6 +240,44 @@ def attention(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, n_q: int,
             out[b, q0:q1] = o.permute(2, 0, 1, 3).reshape(q1 - q0, n_q * hd).to(BF16)
     return out
 
+
+
+def attention_small(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, n_q: int, n_kv: int, hd: int,
+                    sm_scale: float = 1.0) -> torch.Tensor:
+    """The reference's S <= 1024 attention (`attn_fused_small`, mk_jax.py:58-175) -> bf16.
+
+    Rounding points as that kernel writes them: q (carrying the softmax scale, which the reference
+    folds into W_q: bf16(q * sm_scale) here) and k RoPE'd with bf16 products and a bf16 sum
+    (mk_jax.py:86-89, :110-114; the rotate-half matmul with the +-1 permutation is exact); scores f32;
+    masked keys -1e30 (:102-104, :115); the exact row max over all keys (:116); e = exp(s - max) and
+    its sum in f32 (:117-118); P = bf16(e * (1 / sum)) normalised before the PV product (:119-122); PV
+    accumulated in f32 and rounded to bf16 (:131-133).  The reference takes 1 / sum with the TPU's
+    approximate reciprocal (pltpu.reciprocal(approx=True)); this restatement divides exactly.
+    """
+    B, S, _ = qkv.shape
+    g = n_q // n_kv
+    cb, sb = cos[:S].to(F32), sin[:S].to(F32)
+    out = torch.empty((B, S, n_q * hd), dtype=BF16)
+    h2 = hd // 2
+
+    def rope_bf16(x):   # x (S, N, hd) of bf16 values
+        rot = torch.cat([-x[..., h2:], x[..., :h2]], dim=-1)
+        return bf(bf(x * cb[:, None]) + bf(rot * sb[:, None]))
+
+    mask = torch.arange(S)[None, :] > torch.arange(S)[:, None]   # (query, key): key after query
+    for b in range(B):
+        x = qkv[b].to(F32).view(S, n_q + 2 * n_kv, hd)
+        q = rope_bf16(bf(x[:, :n_q] * sm_scale))
+        k = rope_bf16(x[:, n_q:n_q + n_kv])
+        v = x[:, n_q + n_kv:]
+        for h in range(n_q):
+            kh = h // g
+            sc = q[:, h] @ k[:, kh].T                      # (query, key) f32
+            sc = sc.masked_fill(mask, -1e30)
+            e = torch.exp(sc - sc.amax(-1, keepdim=True))
+            p = bf(e * (1.0 / e.sum(-1, keepdim=True)))
+            out[b, :, h * hd:(h + 1) * hd] = (p @ v[:, kh]).to(BF16)
+    return out
 
 # ------------------------------------------------------------------------------------------ model
 def _rms_unit_bf16(x: torch.Tensor, eps: float) -> torch.Tensor:

@@ -10,7 +10,8 @@
     dequantised weights when the quantisation is lossless (exactly representable inputs);
   * fused_qkv: dequantised result within the quantisation error bound of the f32 product
     rmsnorm(x) a (W_q s_w), and exact on an exactly representable case;
-  * attention: the emulation and the FP32 reference vs a brute-force per-query softmax loop;
+  * attention: the emulation and the FP32 reference vs a brute-force per-query softmax loop; the
+    short-sequence restatement (attention_small) by a closed form and the FP32 reference;
   * fused_mlp: the chunk-interleaved W_gu layout gives exactly the same result as the stacked one;
   * last_layer_step equals the last row of the same bf16 layer computed for every token;
   * whole quantized model: within a stated bound of the FP32 golden, argmax identical.
@@ -121,6 +122,35 @@ def test_attention_vs_brute_force():
             assert torch.allclose(ref[0, t, h * hd:(h + 1) * hd], o, atol=1e-5)
             assert torch.allclose(emu[0, t, h * hd:(h + 1) * hd], o, atol=3e-2)
 
+
+
+def test_attention_small_pinned():
+    """attention_small (the reference's S <= 1024 kernel) is pinned by (a) a closed form that separates
+    its rounding points from the long-sequence kernel's: with q = 0 every allowed score is equal, so
+    P = bf16(1 / (t + 1)) on keys 0..t and query t's output is bf16(bf16(1 / (t + 1)) * sum v) -- a
+    restatement that normalised after the PV product, or let a key past the query in, fails; (b) the
+    FP32 reference attention on random inputs, within the bf16 rounding of its RoPE products and P."""
+    from minicpm5_mk.mk_weights import rope_tables
+    from oracle import emulate
+
+    g = torch.Generator().manual_seed(7)
+    S, nq, nkv, hd = 48, 16, 2, 32
+    cos, sin = rope_tables(S, hd, 1e4)
+    qkv = torch.randn(1, S, (nq + 2 * nkv) * hd, generator=g).to(BF16)
+    qkv0 = qkv.clone()
+    qkv0[..., :nq * hd] = 0
+    out = emulate.attention_small(qkv0, cos, sin, nq, nkv, hd).float()
+    v = qkv0[0].float().view(S, nq + 2 * nkv, hd)[:, nq + nkv:]
+    for t in range(S):
+        p = torch.tensor(1.0 / (t + 1)).to(BF16).float()
+        for h in (0, 9):
+            want = (p * v[:t + 1, h // (nq // nkv)].sum(0)).to(BF16).float()
+            assert torch.equal(out[0, t, h * hd:(h + 1) * hd], want), (t, h)
+    sm = 1.0 / math.sqrt(hd)
+    ref = emulate.attention_fp32(qkv, cos, sin, nq, nkv, hd, sm, chunk=16)
+    small = emulate.attention_small(qkv, cos, sin, nq, nkv, hd, sm).float()
+    err = (small - ref).abs()
+    assert err.max() <= 0.02 and err.mean() <= 1e-3, (float(err.max()), float(err.mean()))
 
 def test_fused_mlp_interleave_invariant():
     from minicpm5_mk.mk_weights import interleave_gu, quantize_w
