@@ -142,6 +142,34 @@ def test_short_seq_vs_emulator(name, B, S):
     m.close()
 
 
+
+@pytest.mark.parametrize("name,hd,S", [("tiny-hd96", 96, 12288), ("tiny", 128, 9216)])
+def test_long_seq_vs_emulator(name, hd, S):
+    """Sequences past 8192 tokens: the last-token attention merges S / 64 chunk partials, 1024 / hd groups
+    of chunks with their first 16 loads issued up front; 192 chunks at hd 96 and 144 at hd 128 also take
+    the loop over the chunks beyond those (mk_attn_* serve any multiple of 1024 up to max_seq)."""
+    import dataclasses
+
+    from minicpm5_mk.config import preset
+    from minicpm5_mk.synth import random_hf_state_dict, random_token_ids
+    from oracle import emulate
+
+    dev = _dev()
+    cfg = dataclasses.replace(preset(name), head_dim=hd, name=f"{name}-s{S}")
+    quant = "int8d:qkv+gu|sq|lastbf16|fqkv|fmlp"
+    print(f"[long] {name} hd={hd} S={S}", flush=True)
+    sd = random_hf_state_dict(cfg)
+    ids = random_token_ids(1, S, seed=S)
+    m, w = _build(cfg, quant, sd, S, dev)
+    _, lg = m.forward(ids.reshape(-1).to(dev), 1, S, logits=True)
+    lg = lg.cpu()
+    _, lg_ref = emulate.mk_forward(ids, w, sd["model.embed_tokens.weight"], sd["model.norm.weight"], cfg, quant,
+                                   sd["lm_head.weight"])
+    err = (lg - lg_ref).abs()
+    print(f"[long] logits max {err.max():.4g} mean {err.mean():.4g}", flush=True)
+    assert err.max() <= 0.05 and err.mean() <= 5e-3
+    m.close()
+
 # (preset, logits max-abs tolerance vs FP32, mean-abs tolerance): 2x the error of the CPU emulation of
 # the same W8A8 numerics (oracle/emulate.mk_forward) vs the FP32 golden at (1, 8192):
 #   1b       max 0.216  mean 0.0359  mean|dlogprob| top-20 0.050
