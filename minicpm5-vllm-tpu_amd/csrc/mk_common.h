@@ -77,6 +77,12 @@ __device__ inline f32x16 mfma_bf16_32x32x16(const u32x4& a, const u32x4& b, cons
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(bitcast<bf16x8>(a), bitcast<bf16x8>(b), c, 0, 0, 0);
 }
 
+// 16x16 tile, 32 bf16 of k: lane l holds row / column (l % 16) and k elements 8 (l / 16) .. + 7; the
+// accumulator: lane l holds column (l % 16), rows 4 (l / 16) + j in register j.
+__device__ inline f32x4 mfma_bf16_16x16x32(const u32x4& a, const u32x4& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(bitcast<bf16x8>(a), bitcast<bf16x8>(b), c, 0, 0, 0);
+}
+
 __device__ inline i32x16 mfma_i8_32x32x32(const u32x4& a, const u32x4& b, const i32x16& c) {
   return __builtin_amdgcn_mfma_i32_32x32x32_i8(bitcast<i32x4>(a), bitcast<i32x4>(b), c, 0, 0, 0);
 }
