@@ -294,8 +294,8 @@ def main():
                     help="only the per-kernel timing loops + a 256 MiB device copy (rocprofv3 --pmc calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported (DP / SP sharding is "
-              "described in DESIGN.md but not built)", file=sys.stderr)
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported (data- and "
+              "sequence-parallel sharding over several GPUs is not built)", file=sys.stderr)
         sys.exit(2)
 
     import torch

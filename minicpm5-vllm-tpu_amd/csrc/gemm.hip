@@ -814,14 +814,21 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny16_kernel(GemmArgs g
 }
 
 // Sum of the split-K partials in split order, then the epilogue.
+// Every partial is loaded before the first add (one memory latency, not one per group of loads).
+constexpr int SK_MAX_SPLITS = 16;
+
 template <Epi EPI>
 __global__ __launch_bounds__(256) void skinny_reduce_kernel(GemmArgs g, int splits, const float* part) {
   const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= (size_t)g.M * g.N) return;
   const int m = (int)(i / g.N), n = (int)(i % g.N);
+  float pv[SK_MAX_SPLITS];
+#pragma unroll
+  for (int s = 0; s < SK_MAX_SPLITS; ++s) pv[s] = part[((size_t)min(s, splits - 1) * g.M + m) * g.N + n];   // no branches
   float v = 0.f;
-#pragma unroll 4
-  for (int s = 0; s < splits; ++s) v += part[((size_t)s * g.M + m) * g.N + n];   // in split order
+#pragma unroll
+  for (int s = 0; s < SK_MAX_SPLITS; ++s)
+    if (s < splits) v += pv[s];   // in split order
   epi_store<EPI>(g, m, n, v);
 }
 
@@ -903,7 +910,7 @@ void launch_t(const GemmArgs& g, hipStream_t st) {
 int skinny_splits(const GemmArgs& g, int esz) {
   if (!g.ws || g.epi == Epi::I32) return 1;
   const int nb = (g.N + 31) / 32, Kb = g.K * esz;
-  int sp = std::max(1, std::min(std::min(2048 / std::max(nb, 1), Kb / 512), 16));
+  int sp = std::max(1, std::min(std::min(2048 / std::max(nb, 1), Kb / 512), SK_MAX_SPLITS));
   while (sp > 1 && (size_t)sp * 32 * g.N * sizeof(float) > g.ws_bytes) --sp;
   return sp;
 }

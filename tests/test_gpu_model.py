@@ -9,8 +9,8 @@
     config below (about 2x the CPU emulator's own W8A8 error vs FP32).
   * full architectures at (1, 8192): libmk vs full-size fixtures of the CPU emulation of the same W8A8
     numerics (tests/golden/emulate_*.npz, tests/golden/make_emulator_fixture.py), bounded tightly.
-  * batch invariance at the reference's batch shapes (B, 8192), B = 4..32 (BASELINE configs 4 and 5,
-    the reference's batch gate, benchmark/run_benchmark.py:714-727): every row of the batch equals the
+  * batch invariance at the reference's batch shapes (B, 8192), B = 4..32 for 1B-hd96 and 2B (the
+    reference's batch gate, benchmark/run_benchmark.py:714-727): every row of the batch equals the
     same sequence run alone, bitwise, and row 0 (the golden's sequence) meets the golden checks.
   * batch invariance at tiny size, and hipGraph replay equals eager launches, bitwise.
   * the reference-signature op `runtime.forward` (model.py:749-751): 29 arguments, padded ids,
@@ -312,7 +312,7 @@ def test_two_layer_full_size_vs_emulator(name):
 TWO_LAYER = {"1b": (0.07, 0.012), "1b-hd96": (0.08, 0.012), "2b": (0.15, 0.023)}
 
 
-# (preset, batch sizes): BASELINE configs 4 (1B-hd96, B = 4..32) and 5 (2B), plus the reference's 1B; 2B at
+# (preset, batch sizes): the 1B-hd96 and 2B prefill workloads at B = 4..32, plus the reference's 1B; 2B at
 # B = 48 runs in two chunks (42 + 6 sequences: the (T, I) bf16 activation of 48 x 8192 tokens exceeds 4 GiB).
 BATCH = [("1b-hd96", 4), ("1b-hd96", 8), ("1b-hd96", 16), ("1b-hd96", 32), ("1b", 4), ("1b", 32), ("2b", 4), ("2b", 32),
          ("2b", 48)]
@@ -360,7 +360,7 @@ def test_short_prompt_batch_invariance(name):
 
 
 def test_full_model_bf16_1b_hd96_argmax():
-    """BASELINE config 1 (1B-hd96): the same model with every linear in bf16 (quant "bf16"), to separate
+    """The 1B-hd96 golden forward's model with every linear in bf16 (quant "bf16"), to separate
     the W8A8 numerics from the kernels in the top-1 decision (golden top-1 / top-2 margin 0.029)."""
     from minicpm5_mk.synth import random_token_ids
 
