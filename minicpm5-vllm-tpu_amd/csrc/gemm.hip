@@ -34,7 +34,8 @@ constexpr int BKB = 64;   // K bytes per LDS stage (two MFMA k-steps)
 template <int BM_, int BN_, int WGM_, int WGN_, int NST_, int OCC_, int LOOP_ = 0>
 struct GemmCfg {
   static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_, NST = NST_, OCC = OCC_;
-  // main loop: 0 split k-step pipeline, 1 ping-pong (two wave groups, operand prefetch)
+  // main loop: 0 split k-step pipeline, 1 ping-pong (two wave groups, operand prefetch), 2 two stages
+  // per barrier with the operands read half a stage ahead
   static constexpr int LOOP = LOOP_;
   static constexpr int NW = WGM * WGN, NTH = 64 * NW;
   static constexpr int WM = BM / WGM, WN = BN / WGN;     // wave tile
@@ -51,7 +52,8 @@ struct GemmCfg {
   static_assert(WN % 32 == 0, "wave tile width");
   // ping-pong: waves w and w + 4 share a SIMD and belong to groups 0 and 1; each group loads a uniform
   // number of blocks per stage
-  static_assert(LOOP == 0 || (NW == 8 && NST >= 3 && NQH % 4 == 0),
+  static_assert(LOOP != 2 || NST >= 5, "two-stage loop: stages it + 2, it + 3 land while it + 4 .. are in flight");
+  static_assert(LOOP != 1 || (NW == 8 && NST >= 3 && NQH % 4 == 0),
                 "ping-pong needs two groups of four waves with uniform loads and two stages in flight");
 };
 // 256x256 block, 128x128 per wave (accumulators in AGPRs), one workgroup per CU
@@ -67,8 +69,9 @@ using CfgX = GemmCfg<256, 256, 2, 4, 4, 1, 1>;
 using CfgN = GemmCfg<256, 192, 4, 2, 4, 1, 1>;
 // Short problems (few tiles, each K loop latency-bound): 8-stage rings, seven stages of loads in flight.
 // 128x128 block, 64x64 per wave; 64x128 block, 32x64 per wave; one workgroup per CU
+// (the 64x128 tile runs two stages per barrier: its waves have few MFMAs per stage to cover a barrier)
 using CfgD = GemmCfg<128, 128, 2, 2, 8, 1>;
-using CfgE = GemmCfg<64, 128, 2, 2, 8, 1>;
+using CfgE = GemmCfg<64, 128, 2, 2, 8, 1, 2>;
 
 template <GemmIn IN>
 struct Mma;
@@ -210,23 +213,13 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
     else if (j < C::QL || qfull) copy16_to_lds(Bg + kb + loff[j], dst);
   };
   // wait until at most `n` stages of this wave's async loads are outstanding
-  auto wait_stages = [&](int n) {
-    if (C::QH == C::QL || qfull) {
-      switch (n) {
-        case 0: MK_WAIT_VMCNT(0); break;
-        case 1: MK_WAIT_VMCNT(C::QH); break;
-        case 2: MK_WAIT_VMCNT(2 * C::QH); break;
-        default: MK_WAIT_VMCNT(3 * C::QH); break;
-      }
-    } else {
-      switch (n) {
-        case 0: MK_WAIT_VMCNT(0); break;
-        case 1: MK_WAIT_VMCNT(C::QL); break;
-        case 2: MK_WAIT_VMCNT(2 * C::QL); break;
-        default: MK_WAIT_VMCNT(3 * C::QL); break;
-      }
-    }
+  auto wait_stages = [&](auto nc) {
+    constexpr int n = decltype(nc)::value;
+    static_assert(n * C::QH <= 63, "vmcnt counts at most 63 loads");
+    if (C::QH == C::QL || qfull) MK_WAIT_VMCNT(n * C::QH);
+    else MK_WAIT_VMCNT(n * C::QL);
   };
+  using W0 = std::integral_constant<int, 0>;
 
   Acc acc[C::MT][C::NTL];
 #pragma unroll
@@ -306,14 +299,17 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
   if (EARLY_SCALES && dq) load_scales();
 
   const int nk = Kb / BKB;
+  // stages loaded ahead of the main loop: NST - 1 (NST - 2 for the two-stage loop, whose iterations
+  // load two stages each); stage 0 (stages 0 and 1) visible after the barrier
+  constexpr int PRE = C::LOOP == 2 ? C::NST - 2 : C::NST - 1;
 #pragma unroll
-  for (int s0 = 0; s0 < C::NST - 1; ++s0)
+  for (int s0 = 0; s0 < PRE; ++s0)
     if (s0 < nk) {
 #pragma unroll
       for (int j = 0; j < Q; ++j) issue1(j, s0, s0 * BKB);
     }
-  if (nk >= C::NST - 1) wait_stages(C::NST - 2);
-  else wait_stages(0);
+  if (nk >= PRE) wait_stages(std::integral_constant<int, C::LOOP == 2 ? PRE - 2 : PRE - 1>{});
+  else wait_stages(W0{});
   lds_barrier();
   // Materialize the epilogue's kernel arguments now: a scalar load still pending inside the loop would
   // turn every LDS wait there into lgkmcnt(0) (scalar loads return out of order).
@@ -341,8 +337,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
       acc[mt][nt] = T::run(src[C::NTL + mt], src[nt], acc[mt][nt]);
     };
     // stages 0 and 1 visible; stage 0 in H0 / H1
-    if (nk >= D) wait_stages(D - 2);
-    else wait_stages(0);
+    if (nk >= D) wait_stages(std::integral_constant<int, D - 2>{});
+    else wait_stages(W0{});
     lds_barrier();
 #pragma unroll
     for (int q = 0; q < NOP; ++q) rdq(smem, 0, q, H0);
@@ -416,6 +412,80 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
       if (it + 2 < nk) step(Tail{}, it + 2, H1, H2, H0);
     }
     if (wgrp == 0) lds_barrier();
+  } else if constexpr (C::LOOP == 2) {
+    // Two stages per iteration and one barrier.  Operand sets X0 .. X3 hold (stage it, k-step 0),
+    // (it, 1), (it + 1, 0), (it + 1, 1); each set is read from LDS while the MFMAs of the previous one
+    // run, and X0 of the next iteration is read right after the barrier, under the MFMAs of X3.  The
+    // loads of stages it + NST - 2 and it + NST - 1 go to the slots of stages it - 2 and it - 1, which
+    // every wave finished reading before the last barrier (lgkmcnt(0) ahead of it).  The MFMAs of an
+    // output element run over the k-steps in the same order as in the other loops.
+    static_assert(C::QH == C::QL, "uniform loads per wave");
+    u32x4 xa0[C::MT], xb0[C::NTL], xa1[C::MT], xb1[C::NTL], xa2[C::MT], xb2[C::NTL], xa3[C::MT], xb3[C::NTL];
+    rd(smem, ao0, bo0, xa0, xb0);
+    int cur = 0;   // slot of stage it
+    auto slot = [&](int d) { return cur + d < C::NST ? cur + d : cur + d - C::NST; };
+    auto iter2 = [&](auto steady, int it) {
+      constexpr bool ST = decltype(steady)::value;
+      const char* S0 = smem + cur * C::ST_BYTES;
+      const char* S1 = smem + slot(1) * C::ST_BYTES;
+      const bool two = ST || it + 1 < nk;
+      const bool pre0 = ST || it + C::NST - 2 < nk, pre1 = ST || it + C::NST - 1 < nk;
+      const int ns0 = slot(C::NST - 2), ns1 = slot(C::NST - 1);
+      rd(S0, ao1, bo1, xa1, xb1);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < NMF; ++i) {
+        mf(i, xa0, xb0);
+        if (i < Q && pre0) issue1(i, ns0, (it + C::NST - 2) * BKB);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (Q > NMF && pre0) {
+#pragma unroll
+        for (int j = NMF; j < Q; ++j) issue1(j, ns0, (it + C::NST - 2) * BKB);
+      }
+      if (two) rd(S1, ao0, bo0, xa2, xb2);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < NMF; ++i) {
+        mf(i, xa1, xb1);
+        if (i < Q && pre1) issue1(i, ns1, (it + C::NST - 1) * BKB);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (Q > NMF && pre1) {
+#pragma unroll
+        for (int j = NMF; j < Q; ++j) issue1(j, ns1, (it + C::NST - 1) * BKB);
+      }
+      if (two) {
+        rd(S1, ao1, bo1, xa3, xb3);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < NMF; ++i) {
+          mf(i, xa2, xb2);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      cur = slot(2);
+      if (ST || it + 2 < nk) {
+        // stages it + 2 and it + 3 landed for this wave, then for every wave; this wave's reads of
+        // stages it and it + 1 are done
+        if (ST) MK_WAIT_VMCNT((C::NST - 4) * Q);
+        else MK_WAIT_VMCNT(0);
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        lds_barrier();
+        rd(smem + cur * C::ST_BYTES, ao0, bo0, xa0, xb0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (two) {
+#pragma unroll
+        for (int i = 0; i < NMF; ++i) {
+          mf(i, xa3, xb3);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    };
+    int it = 0;
+    for (; it + C::NST - 1 < nk; it += 2) iter2(std::integral_constant<bool, true>{}, it);
+    for (; it < nk; it += 2) iter2(std::integral_constant<bool, false>{}, it);
   } else {
     u32x4 ra0[C::MT], rb0[C::NTL], ra1[C::MT], rb1[C::NTL];
     rd(smem, ao0, bo0, ra0, rb0);
@@ -847,7 +917,7 @@ int choose_cfg(const GemmArgs& g) {
   if (forced >= 1 && forced <= 7 && !(silu && forced == 5)) return forced;
   // Few tiles, long K loop (short prompts, e.g. M = 1024 - 2048 with the bf16 O / down projections): each
   // 64-byte stage costs a memory latency more than its MFMAs, so the deep rings win (measured on MI355X:
-  // the 1B down projection at M = 1024 takes 33.8 us on 64x128, 40.4 on 128x128 deep, 48.4 on the 128x128
+  // the 1B down projection at M = 1024 takes 31.9 us on 64x128, 40.3 on 128x128 deep, 48.4 on the 128x128
   // three-workgroup tile); with < 64 stages the per-tile fixed cost dominates and the wide tiles stay best.
   {
     const int nk = g.K * (g.in == GemmIn::BF16 ? 2 : 1) / BKB;

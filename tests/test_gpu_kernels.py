@@ -247,6 +247,21 @@ def test_gemm_bf16(M, N, K):
     assert ((outb - ref).abs() <= ref.abs() * 2.0 ** -8 + 1e-3 * ref.abs().max()).all()
 
 
+@pytest.mark.parametrize("N,K", [(1536, 4608), (1536, 2080)])
+def test_gemm_bf16_rows_independent_of_tile(N, K):
+    """The first 1000 rows of a 4096-row product take the 64x128 short-problem tile (its two-stage loop,
+    an odd stage count at K = 2080) alone and a wide tile inside the big product: identical f32 bits."""
+    from minicpm5_mk import ops
+
+    dev = _dev()
+    g = torch.Generator().manual_seed(K)
+    a = torch.randn(4096, K, generator=g).to(BF16).to(dev)
+    b = (torch.randn(N, K, generator=g) * 0.02).to(BF16).to(dev)
+    big = ops.gemm(a, b, "f32")
+    small = ops.gemm(a[:1000].contiguous(), b, "f32")
+    assert torch.equal(small.view(torch.int32), big[:1000].view(torch.int32))
+
+
 def test_gemm_residual_epilogues():
     from minicpm5_mk import ops
 
