@@ -164,12 +164,35 @@ __device__ inline float xhalf_sum(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Spare workgroup j of np (a launch with fewer work items than CUs): 16-byte loads over the ranges, in
+// order, PF_U in flight per lane, folded into one word that is stored only through `sink`, which the
+// launcher passes as null (so the loads stay).  Indices are clamped to a range's last vector.
+constexpr int PF_U = 16;
+template <int NTH>
+__device__ void prefetch_ranges(const PrefetchRanges& pf, int j, int np, int tid, uint32_t* sink) {
+  uint32_t acc = 0;
+  const size_t stride = (size_t)np * NTH;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const size_t n16 = pf.bytes[r] / 16;
+    const u32x4* base = static_cast<const u32x4*>(pf.p[r]);
+    for (size_t i = (size_t)j * NTH + tid; i < n16; i += stride * PF_U) {
+      u32x4 v[PF_U];
+#pragma unroll
+      for (int u = 0; u < PF_U; ++u) v[u] = base[min(i + u * stride, n16 - 1)];
+#pragma unroll
+      for (int u = 0; u < PF_U; ++u) acc ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
+    }
+  }
+  if (sink) sink[0] = acc;
+}
+
 template <int HD, bool DYN, int GW>
 __global__ __launch_bounds__(64 * GW, 1) void attn_fwd_kernel(
     const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ cosr,
     const uint16_t* __restrict__ sinr, const uint16_t* __restrict__ krope,
     const uint16_t* __restrict__ vt, uint16_t* __restrict__ out, int B, int S, int n_q, int n_kv,
-    float qscale, int* __restrict__ queue) {
+    float qscale, int* __restrict__ queue, PrefetchRanges pf, int n_work, uint32_t* pf_sink) {
   using L = AttnSmem<HD>;
   constexpr int KS = HD / 16;   // k-steps of QK^T
   constexpr int DT = HD / 32;   // 32-row d tiles of O^T
@@ -262,6 +285,10 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_fwd_kernel(
     }
   };
 
+  // workgroups n_work.. of a queue launch only prefetch (the launch's spare CUs), then count out below
+  if (DYN && (int)blockIdx.x >= n_work)
+    prefetch_ranges<64 * GW>(pf, blockIdx.x - n_work, gridDim.x - n_work, tid, pf_sink);
+  else
   for (int pass = 0;; ++pass) {
     int kv, qt, b, hg;
     if constexpr (DYN) {
@@ -608,15 +635,32 @@ int launch_attn_hd(const AttnArgs& a, hipStream_t st, int stages) {
     // pairs when they fill the CUs in whole rounds (no queue atomics, fixed XCD placement), else the work
     // queues.
     const int items8 = a.B * a.n_kv * (a.S / QT);
+    // the prefetch ranges shrunk to the whole 16-byte vectors inside them
+    PrefetchRanges pf{};
+    bool any_pf = false;
+    for (int r = 0; r < 4; ++r) {
+      if (!a.pf.p[r] || a.pf.bytes[r] < 32) continue;
+      const uintptr_t b0 = reinterpret_cast<uintptr_t>(a.pf.p[r]), e0 = b0 + a.pf.bytes[r];
+      const uintptr_t b16 = (b0 + 15) & ~(uintptr_t)15, e16 = e0 & ~(uintptr_t)15;
+      pf.p[r] = reinterpret_cast<const void*>(b16);
+      pf.bytes[r] = e16 - b16;
+      any_pf = true;
+    }
     auto go = [&](auto gw) {
       constexpr int GW = decltype(gw)::value;
       const int items = items8 * (G / GW), pairs = items / 2;
       if (pairs % ncu == 0) {
         hipLaunchKernelGGL((attn_fwd_kernel<HD, false, GW>), dim3(pairs), dim3(64 * GW), 0, st, a.qkv, a.cos,
-                           a.sin, a.krope, a.vt, a.out, a.B, a.S, a.n_q, a.n_kv, a.qscale, queue);
+                           a.sin, a.krope, a.vt, a.out, a.B, a.S, a.n_q, a.n_kv, a.qscale, queue, pf, pairs,
+                           (uint32_t*)nullptr);
       } else {
-        hipLaunchKernelGGL((attn_fwd_kernel<HD, true, GW>), dim3(items < ncu ? items : ncu), dim3(64 * GW), 0, st,
-                           a.qkv, a.cos, a.sin, a.krope, a.vt, a.out, a.B, a.S, a.n_q, a.n_kv, a.qscale, queue);
+        // one persistent workgroup per CU, at most one per item; with prefetch ranges, the CUs left over
+        // get prefetch-only workgroups
+        const int nwork = items < ncu ? items : ncu;
+        const int grid = any_pf ? ncu : nwork;
+        hipLaunchKernelGGL((attn_fwd_kernel<HD, true, GW>), dim3(grid), dim3(64 * GW), 0, st, a.qkv, a.cos, a.sin,
+                           a.krope, a.vt, a.out, a.B, a.S, a.n_q, a.n_kv, a.qscale, queue, pf, nwork,
+                           (uint32_t*)nullptr);
       }
     };
     if (items8 < ncu) go(std::integral_constant<int, 4>{});

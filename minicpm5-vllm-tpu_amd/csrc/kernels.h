@@ -8,6 +8,13 @@
 namespace mk {
 
 // ------------------------------------------------------------------------------ attention
+// Byte ranges that otherwise idle workgroups of a launch read and drop (attn.hip): a hint that leaves the
+// data in the memory-side cache for the launches that follow.  No result depends on it.
+struct PrefetchRanges {
+  const void* p[4];
+  size_t bytes[4];   // 0: unused
+};
+
 struct AttnArgs {
   const uint16_t* qkv;   // (B, S, (n_q + 2 n_kv) hd) bf16, token-major, [q heads | k heads | v heads]
   const uint16_t* cos;   // (>= S, hd) bf16 RoPE table
@@ -18,6 +25,7 @@ struct AttnArgs {
   int B, S, n_q, n_kv, hd;
   float qscale;          // multiplies RoPE'd q before the bf16 rounding (sm_scale * log2 e)
   int k_pairs;           // 1: qkv's K columns are in RoPE pair groups (pack.hip map 2), 0: the reference order
+  PrefetchRanges pf;     // read by the spare workgroups of a launch with fewer work items than CUs
 };
 int attn_validate(int B, int S, int n_q, int n_kv, int hd);
 size_t attn_scratch_bytes(int B, int S, int n_kv, int hd);
