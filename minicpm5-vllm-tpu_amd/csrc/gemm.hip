@@ -915,14 +915,15 @@ int choose_cfg(const GemmArgs& g) {
     return e ? std::atoi(e) : 0;
   }();
   if (forced >= 1 && forced <= 7 && !(silu && forced == 5)) return forced;
-  // Few tiles, long K loop (short prompts, e.g. M = 1024 - 2048 with the bf16 O / down projections): each
-  // 64-byte stage costs a memory latency more than its MFMAs, so the deep rings win (measured on MI355X:
-  // the 1B down projection at M = 1024 takes 31.9 us on 64x128, 40.3 on 128x128 deep, 48.4 on the 128x128
-  // three-workgroup tile); with < 64 stages the per-tile fixed cost dominates and the wide tiles stay best.
+  // Few tiles (short prompts, e.g. M <= 1024): each tile's K loop is latency-bound, so the 64x128 tile
+  // whose loop runs two stages per barrier wins whenever its tiling fits one round of 256 CUs (measured
+  // on MI355X at M = 128 - 1024: the 1B gate/up at M = 128 takes 7.6 us on it, 14.0 on 256x128; the 1B
+  // down at M = 1024 31.9 us, 40.3 on the 128x128 deep ring, 48.4 on the 128x128 three-workgroup
+  // tile); otherwise the 128x128 deep ring for long K loops, else the wide tiles.
   {
     const int nk = g.K * (g.in == GemmIn::BF16 ? 2 : 1) / BKB;
     auto tiles = [&](int bm, int bn) { return (long)((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn); };
-    if (nk >= 64 && tiles(64, 128) <= 256) return 7;
+    if (nk >= 16 && tiles(64, 128) <= 256) return 7;
     if (nk >= 64 && tiles(128, 128) <= 256) return 6;
   }
   struct Opt { int id, bm, bn; double eff; };
