@@ -192,7 +192,7 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_fwd_kernel(
     const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ cosr,
     const uint16_t* __restrict__ sinr, const uint16_t* __restrict__ krope,
     const uint16_t* __restrict__ vt, uint16_t* __restrict__ out, int B, int S, int n_q, int n_kv,
-    float qscale, int* __restrict__ queue, PrefetchRanges pf, int n_work, uint32_t* pf_sink) {
+    float qscale, int* __restrict__ queue, PrefetchRanges pf, int n_work, int direct, uint32_t* pf_sink) {
   using L = AttnSmem<HD>;
   constexpr int KS = HD / 16;   // k-steps of QK^T
   constexpr int DT = HD / 32;   // 32-row d tiles of O^T
@@ -216,7 +216,8 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_fwd_kernel(
   //    serves one kv head's K / V^T stream.  Used when the pairs fill the CUs in whole rounds.
   //  * DYN: one persistent workgroup per CU takes items from one queue per kv head (an atomic
   //    counter), longest tiles first: from the queue of its XCD's kv head (XCD id mod n_kv) and, when
-  //    that one is empty, from the others.  Used for short or odd-sized launches.
+  //    that one is empty, from the others.  Used for short or odd-sized launches; with no more items
+  //    than CUs (`direct`), workgroup i computes item i and the queues are not touched.
   constexpr int NHG = G / GW;                        // head groups per kv head
   const int ntiles = S / QT;
   const int nper = B * ntiles * NHG;                 // items per kv head
@@ -292,21 +293,28 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_fwd_kernel(
   for (int pass = 0;; ++pass) {
     int kv, qt, b, hg;
     if constexpr (DYN) {
-      if (tid == 0) {
-        int it = -1;
-        for (int k = 0; k < n_kv; ++k) {
-          const int q = (xq + k) % n_kv;
-          const int v = atomicAdd(&queue[q], 1);
-          if (v >= 0 && v < nper) {
-            it = q * nper + v;
-            break;
+      int item;
+      if (direct) {
+        // a workgroup for every item: the item is the workgroup index, no queue atomics
+        if (pass == 1) break;
+        item = blockIdx.x;
+      } else {
+        if (tid == 0) {
+          int it = -1;
+          for (int k = 0; k < n_kv; ++k) {
+            const int q = (xq + k) % n_kv;
+            const int v = atomicAdd(&queue[q], 1);
+            if (v >= 0 && v < nper) {
+              it = q * nper + v;
+              break;
+            }
           }
+          *item_s = it;
         }
-        *item_s = it;
+        __syncthreads();
+        item = __builtin_amdgcn_readfirstlane(*item_s);
+        if (item < 0) break;
       }
-      __syncthreads();
-      const int item = __builtin_amdgcn_readfirstlane(*item_s);
-      if (item < 0) break;
       kv = item / nper;
       const int v = item % nper;                     // longest tiles first
       qt = ntiles - 1 - v / (B * NHG);
@@ -603,7 +611,7 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_fwd_kernel(
   }
   // the last workgroup out resets the queues for the next launch; the fence orders this workgroup's
   // queue atomics before its count
-  if (DYN && tid == 0) {
+  if (DYN && !direct && tid == 0) {
     __threadfence();
     const int done = atomicAdd(&queue[n_kv], 1);
     if (done == (int)(gridDim.x * gridDim.y * gridDim.z) - 1) {
@@ -651,16 +659,16 @@ int launch_attn_hd(const AttnArgs& a, hipStream_t st, int stages) {
       const int items = items8 * (G / GW), pairs = items / 2;
       if (pairs % ncu == 0) {
         hipLaunchKernelGGL((attn_fwd_kernel<HD, false, GW>), dim3(pairs), dim3(64 * GW), 0, st, a.qkv, a.cos,
-                           a.sin, a.krope, a.vt, a.out, a.B, a.S, a.n_q, a.n_kv, a.qscale, queue, pf, pairs,
+                           a.sin, a.krope, a.vt, a.out, a.B, a.S, a.n_q, a.n_kv, a.qscale, queue, pf, pairs, 0,
                            (uint32_t*)nullptr);
       } else {
-        // one persistent workgroup per CU, at most one per item; with prefetch ranges, the CUs left over
-        // get prefetch-only workgroups
+        // one persistent workgroup per CU taking items from the queues, or, with no more items than CUs, one
+        // workgroup per item (no queues); with prefetch ranges, the CUs left over get prefetch-only workgroups
         const int nwork = items < ncu ? items : ncu;
         const int grid = any_pf ? ncu : nwork;
         hipLaunchKernelGGL((attn_fwd_kernel<HD, true, GW>), dim3(grid), dim3(64 * GW), 0, st, a.qkv, a.cos, a.sin,
                            a.krope, a.vt, a.out, a.B, a.S, a.n_q, a.n_kv, a.qscale, queue, pf, nwork,
-                           (uint32_t*)nullptr);
+                           nwork == items ? 1 : 0, (uint32_t*)nullptr);
       }
     };
     if (items8 < ncu) go(std::integral_constant<int, 4>{});
