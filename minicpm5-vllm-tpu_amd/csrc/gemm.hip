@@ -414,24 +414,27 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
     if (wgrp == 0) lds_barrier();
   } else if constexpr (C::LOOP == 2) {
     // Two stages per iteration and one barrier.  Operand sets X0 .. X3 hold (stage it, k-step 0),
-    // (it, 1), (it + 1, 0), (it + 1, 1); each set is read from LDS while the MFMAs of the previous one
-    // run, and X0 of the next iteration is read right after the barrier, under the MFMAs of X3.  The
-    // loads of stages it + NST - 2 and it + NST - 1 go to the slots of stages it - 2 and it - 1, which
-    // every wave finished reading before the last barrier (lgkmcnt(0) ahead of it).  The MFMAs of an
-    // output element run over the k-steps in the same order as in the other loops.
+    // (it, 1), (it + 1, 0), (it + 1, 1).  X2 and X3 are read at the top of the iteration, under the
+    // MFMAs of X0 and X1; X0 and X1 of the next iteration right after the barrier, under the MFMAs of X3.
+    // The loads of stages it + NST - 2 and it + NST - 1 go to the slots of stages it - 2 and it - 1,
+    // which every wave finished reading before the last barrier (lgkmcnt(0) ahead of it).  The MFMAs of
+    // an output element run over the k-steps in the same order as in the other loops.
     static_assert(C::QH == C::QL, "uniform loads per wave");
     u32x4 xa0[C::MT], xb0[C::NTL], xa1[C::MT], xb1[C::NTL], xa2[C::MT], xb2[C::NTL], xa3[C::MT], xb3[C::NTL];
     rd(smem, ao0, bo0, xa0, xb0);
+    rd(smem, ao1, bo1, xa1, xb1);
     int cur = 0;   // slot of stage it
     auto slot = [&](int d) { return cur + d < C::NST ? cur + d : cur + d - C::NST; };
     auto iter2 = [&](auto steady, int it) {
       constexpr bool ST = decltype(steady)::value;
-      const char* S0 = smem + cur * C::ST_BYTES;
       const char* S1 = smem + slot(1) * C::ST_BYTES;
       const bool two = ST || it + 1 < nk;
       const bool pre0 = ST || it + C::NST - 2 < nk, pre1 = ST || it + C::NST - 1 < nk;
       const int ns0 = slot(C::NST - 2), ns1 = slot(C::NST - 1);
-      rd(S0, ao1, bo1, xa1, xb1);
+      if (two) {
+        rd(S1, ao0, bo0, xa2, xb2);
+        rd(S1, ao1, bo1, xa3, xb3);
+      }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < NMF; ++i) {
@@ -443,8 +446,6 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
 #pragma unroll
         for (int j = NMF; j < Q; ++j) issue1(j, ns0, (it + C::NST - 2) * BKB);
       }
-      if (two) rd(S1, ao0, bo0, xa2, xb2);
-      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < NMF; ++i) {
         mf(i, xa1, xb1);
@@ -456,8 +457,6 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
         for (int j = NMF; j < Q; ++j) issue1(j, ns1, (it + C::NST - 1) * BKB);
       }
       if (two) {
-        rd(S1, ao1, bo1, xa3, xb3);
-        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < NMF; ++i) {
           mf(i, xa2, xb2);
@@ -472,7 +471,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
         else MK_WAIT_VMCNT(0);
         __builtin_amdgcn_s_waitcnt(0xc07f);
         lds_barrier();
-        rd(smem + cur * C::ST_BYTES, ao0, bo0, xa0, xb0);
+        const char* S2 = smem + cur * C::ST_BYTES;
+        rd(S2, ao0, bo0, xa0, xb0);
+        rd(S2, ao1, bo1, xa1, xb1);
       }
       __builtin_amdgcn_sched_barrier(0);
       if (two) {
