@@ -203,14 +203,18 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
       loff[j] = (uint32_t)min(n0 + r, g.N - 1) * (uint32_t)ldb + 16u * ((lane & 3) ^ swz(r));
     }
   }
-  const char* const Ag = static_cast<const char*>(g.A);
-  const char* const Bg = static_cast<const char*>(g.B);
+  // The operands as buffers for the async loads (buffer_load_dwordx4 ... lds): the lane's offset is loff,
+  // the K offset goes in the instruction's scalar offset.  The buffer form is counted by vmcnt alone, so
+  // the compiler waits for exactly the LDS operand reads an MFMA needs (with the FLAT-encoded global
+  // form in flight it waits for all of them).  Both operands span < 4 GiB (checked by the launcher).
+  const __amdgpu_buffer_rsrc_t rA = make_rsrc(g.A, (uint32_t)((size_t)g.M * lda));
+  const __amdgpu_buffer_rsrc_t rB = make_rsrc(g.B, (uint32_t)((size_t)g.N * ldb));
   // async load j (of Q) of stage `st` at K byte offset kb; block b sits at b KB in the stage (A blocks,
   // then B blocks)
   auto issue1 = [&](int j, int st, int kb) {
     char* dst = smem + st * C::ST_BYTES + (w + C::NW * j) * 1024;
-    if (j < JA) copy16_to_lds(Ag + kb + loff[j], dst);
-    else if (j < C::QL || qfull) copy16_to_lds(Bg + kb + loff[j], dst);
+    if (j < JA) copy16_to_lds(rA, loff[j], (uint32_t)kb, dst);
+    else if (j < C::QL || qfull) copy16_to_lds(rB, loff[j], (uint32_t)kb, dst);
   };
   // wait until at most `n` stages of this wave's async loads are outstanding
   auto wait_stages = [&](auto nc) {
@@ -1078,6 +1082,8 @@ int gemm_validate(const GemmArgs& g) {
   MK_REQUIRE((g.lda * esz) % 16 == 0 && (g.ldb * esz) % 16 == 0 && g.lda >= g.K && g.ldb >= g.K,
              "gemm: operand strides must be >= K and 16-byte aligned");
   MK_REQUIRE(((uintptr_t)g.A % 16) == 0 && ((uintptr_t)g.B % 16) == 0, "gemm: operands must be 16-byte aligned");
+  MK_REQUIRE((size_t)g.M * g.lda * esz < ((size_t)1 << 32) && (size_t)g.N * g.ldb * esz < ((size_t)1 << 32),
+             "gemm: each operand must span < 4 GiB (32-bit offsets)");
   const bool res = g.epi == Epi::RES_BF16ADD || g.epi == Epi::DQ_RES_BF16ADD || g.epi == Epi::RES_F32ADD ||
                    g.epi == Epi::DQ2_RES_F32ADD || g.epi == Epi::DQ2_RES_BF16ADD;
   MK_REQUIRE(res ? (g.res != nullptr && g.ldr >= g.N) : (g.out != nullptr && g.ldo >= 1), "gemm: missing output");
