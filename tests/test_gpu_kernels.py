@@ -106,7 +106,8 @@ def test_attention_batch_invariant(B, S, hd):
     """Each sequence of a batch equals the same sequence run alone, bit for bit.  (2, 4096) and
     (4, 2048) launch 256 tile pairs (B * 2 kv heads * S / 64) and take the static pair mapping;
     (3, 2048) launches 384 items on 256 persistent workgroups, so workgroups take several items and
-    drain the other kv head's queue; the single-sequence runs take the work queues one item each."""
+    drain the other kv head's queue; the single-sequence runs have no more items than CUs and take the
+    direct mapping (workgroup i computes item i, no queue)."""
     from minicpm5_mk import ops
     from minicpm5_mk.mk_weights import rope_tables
 
