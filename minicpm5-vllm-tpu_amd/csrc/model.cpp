@@ -405,19 +405,26 @@ int launch_forward(const Fwd& f, hipStream_t st) {
     aa.hd = c.head_dim;
     aa.qscale = 1.4426950408889634f;
     aa.k_pairs = 1;   // W_qkv is packed with K in RoPE pair groups
-    // The weights of this layer's O, gate/up and down projections and of the next layer's QKV, read into the
-    // memory-side cache by the attention launch's spare workgroups (a short prompt leaves CUs idle there).
-    // The layers' weights together exceed that cache, so otherwise each GEMM of a short prompt streams
-    // its weights cold, a full HBM round trip per 64-byte K stage.
-    aa.pf.p[0] = pb + m.P.wo + (size_t)l * H * qd * e1;
-    aa.pf.bytes[0] = (size_t)H * qd * e1;
-    aa.pf.p[1] = pb + m.P.wgu + (size_t)l * 2 * I * H * e2;
-    aa.pf.bytes[1] = (size_t)2 * I * H * e2;
-    aa.pf.p[2] = pb + m.P.wd + (size_t)l * H * I * e3;
-    aa.pf.bytes[2] = (size_t)H * I * e3;
+    // The weights of this layer's down and O projections, of the next layer's QKV and of this layer's
+    // gate/up, read into the memory-side cache by the attention launch's spare workgroups (a short prompt
+    // leaves CUs idle there).  The layers' weights together exceed that cache, so otherwise each GEMM of a
+    // short prompt streams its weights cold, a full HBM round trip per 64-byte K stage.  Ranges in order of
+    // what a cold start costs (measured: down most, gate/up least), gate/up only within kPrefetchBudget:
+    // more than the attention reads in its own time lengthens the launch (2B at (1, 1024): 6.01 ms with
+    // gate/up's 25 MB, 5.91 ms without; 1B, 14 MB: 2.82 ms with, 2.85 without).
+    constexpr size_t kPrefetchBudget = (size_t)48 << 20;
+    aa.pf.p[0] = pb + m.P.wd + (size_t)l * H * I * e3;
+    aa.pf.bytes[0] = (size_t)H * I * e3;
+    aa.pf.p[1] = pb + m.P.wo + (size_t)l * H * qd * e1;
+    aa.pf.bytes[1] = (size_t)H * qd * e1;
     if (l + 1 < Lm) {
-      aa.pf.p[3] = pb + m.P.wqkv + (size_t)(l + 1) * D * H * e0;
-      aa.pf.bytes[3] = (size_t)D * H * e0;
+      aa.pf.p[2] = pb + m.P.wqkv + (size_t)(l + 1) * D * H * e0;
+      aa.pf.bytes[2] = (size_t)D * H * e0;
+    }
+    const size_t gu_bytes = (size_t)2 * I * H * e2;
+    if (aa.pf.bytes[0] + aa.pf.bytes[1] + aa.pf.bytes[2] + gu_bytes <= kPrefetchBudget) {
+      aa.pf.p[3] = pb + m.P.wgu + (size_t)l * 2 * I * H * e2;
+      aa.pf.bytes[3] = gu_bytes;
     }
 
     GemmArgs g{};
