@@ -187,7 +187,8 @@ def test_row_quant_scale_tree_bitexact(T, H):
     assert np.array_equal(sx.cpu().numpy().view(np.uint32), ref.view(np.uint32))
 
 
-@pytest.mark.parametrize("M,N,K", [(256, 128, 64), (300, 200, 1536), (8192, 1920, 1536), (1000, 1536, 4608)])
+@pytest.mark.parametrize("M,N,K", [(256, 128, 64), (300, 200, 1536), (8192, 1920, 1536), (1000, 1536, 4608),
+                                   (1000, 1536, 1088)])
 def test_gemm_int8_exact(M, N, K):
     from minicpm5_mk import ops
     from oracle import emulate
@@ -248,10 +249,11 @@ def test_gemm_bf16(M, N, K):
     assert ((outb - ref).abs() <= ref.abs() * 2.0 ** -8 + 1e-3 * ref.abs().max()).all()
 
 
-@pytest.mark.parametrize("N,K", [(1536, 4608), (1536, 2080)])
+@pytest.mark.parametrize("N,K", [(1536, 4608), (1536, 2080), (1536, 544)])
 def test_gemm_bf16_rows_independent_of_tile(N, K):
-    """The first 1000 rows of a 4096-row product take the 64x128 short-problem tile (its two-stage loop,
-    an odd stage count at K = 2080) alone and a wide tile inside the big product: identical f32 bits."""
+    """The first 1000 rows of a 4096-row product take the 64x128 short-problem tile (its two-stage loop;
+    odd stage counts at K = 2080 and at K = 544, 17 stages, the fewest it is chosen for) alone and a wide
+    tile inside the big product: identical f32 bits."""
     from minicpm5_mk import ops
 
     dev = _dev()
