@@ -237,7 +237,10 @@ int mk_act_quant(const void* x, int x_f32, const float* a, int T, int H, float e
 #define MK_IN_BF16 0
 #define MK_IN_INT8 1
 #define MK_IN_FP8 2
-/* MFMA GEMM with a fused epilogue; in_type is MK_IN_*. */
+/* MFMA GEMM with a fused epilogue; in_type is MK_IN_*.  A and B 16-byte aligned, lda / ldb >= K in
+ * elements (16-byte multiples), K a multiple of 32 bytes, and each operand spanning < 4 GiB (M lda and
+ * N ldb bytes: 32-bit load offsets); else MK_EINVAL.  Results do not depend on the tile shape the
+ * launcher picks for (M, N, K). */
 int mk_gemm(int in_type, int epi, const void* A, int lda, const void* B, int ldb, int M, int N, int K,
             void* out, int ldo, void* res, int ldr, const float* rs, const float* cs, const float* aux,
             void* stream);

@@ -179,3 +179,18 @@ def test_attn_prefill_rejects_oversized_seq():
     p = ctypes.c_void_p(0x10000)
     rc = lib.mk_attn_prefill(p, p, p, p, p, 1 << 40, 1, 262144, 16, 2, 128, ctypes.c_float(1.0), None)
     assert rc == -1 and b"131072" in lib.mk_last_error()
+
+
+def test_gemm_rejects_operands_of_4_gib():
+    """mk_gemm addresses its operands with 32-bit offsets: an operand of >= 4 GiB is MK_EINVAL before any
+    launch (the pointers here are never dereferenced)."""
+    from minicpm5_mk import _lib
+
+    lib = _lib.load()
+    p = ctypes.c_void_p(0x10000)
+    # A: 40000 rows x 65536 bf16 = 5.2 GB
+    rc = lib.mk_gemm(0, 4, p, 65536, p, 65536, 40000, 256, 65536, p, 256, None, 0, None, None, None, None)
+    assert rc == -1 and b"4 GiB" in lib.mk_last_error()
+    # B: 40000 rows x 65536 bf16
+    rc = lib.mk_gemm(0, 4, p, 65536, p, 65536, 256, 40000, 65536, p, 40000, None, 0, None, None, None, None)
+    assert rc == -1 and b"4 GiB" in lib.mk_last_error()
