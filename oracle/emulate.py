@@ -311,9 +311,12 @@ def last_layer_step(x: torch.Tensor, w: dict, cos, sin, n_q: int, n_kv: int, hd:
 
 @torch.no_grad()
 def mk_forward(ids: torch.Tensor, w: dict, embed: torch.Tensor, final_norm: torch.Tensor, cfg, quant: str,
-               lm_head: torch.Tensor | None = None):
+               lm_head: torch.Tensor | None = None, attn: str = "v2"):
     """ids (B, S) -> (hidden (B, H) bf16, logits (B, V) f32 or None).  `w` is prepare_mk_weights' dict;
-    supports every quant base (bf16, int8d, int8, fp8d, fp8) with the fused (fqkv, fmlp) or XLA algebra."""
+    supports every quant base (bf16, int8d, int8, fp8d, fp8) with the fused (fqkv, fmlp) or XLA algebra.
+    attn: "v2" runs the super_gqa_v2 numerics at every S; "auto" follows the reference's default dispatch
+    (mk_jax.py:341, 364-365): the S <= 1024 kernel (attention_small) at S <= 1024, super_gqa_v2 above."""
+    assert attn in ("v2", "auto"), attn
     from minicpm5_mk.mk_weights import mlp_chunk
     from minicpm5_mk.quant import parse_quant, quant_flags
 
@@ -332,7 +335,10 @@ def mk_forward(ids: torch.Tensor, w: dict, embed: torch.Tensor, final_norm: torc
             qkv = fused_qkv(x, w["w_qkv"][l], w["s_qkv"][l], w["a_qkv"][l], eps)
         else:
             qkv = linear_rmsnorm(x, w["w_qkv"][l], w["s_qkv"][l], w["a_qkv"][l], eps, qm["qkv"])
-        att = attention(qkv.view(B, S, -1), cos, sin, n_q, n_kv, hd).reshape(B * S, -1)
+        if attn == "auto" and S <= 1024:
+            att = attention_small(qkv.view(B, S, -1), cos, sin, n_q, n_kv, hd).reshape(B * S, -1)
+        else:
+            att = attention(qkv.view(B, S, -1), cos, sin, n_q, n_kv, hd).reshape(B * S, -1)
         o = linear(att, w["w_o"][l], w["s_o"][l], w["a_o"][l], qm["o"])
         x = bf(x.to(F32) + o.to(F32)).to(BF16)
         if fmlp:

@@ -224,6 +224,38 @@ def test_quantized_model_close_to_fp32_golden(quant):
     assert torch.equal(lg.argmax(-1), gold.argmax(-1))
 
 
+def test_reference_attention_dispatch():
+    """emulate.mk_forward(attn="auto") follows the reference's default attention choice (mk_jax.py:341,
+    364-365): the S <= 1024 kernel (attention_small) at S <= 1024 -- its logits differ from the v2
+    numerics' and, like them, stay within 0.05 of the FP32 golden with the same argmax -- and
+    super_gqa_v2 at S >= 2048, identical to attn="v2"."""
+    import os
+
+    from minicpm5_mk.config import preset
+    from minicpm5_mk.mk_weights import prepare_mk_weights
+    from minicpm5_mk.synth import random_hf_state_dict, random_token_ids
+    from oracle import emulate
+
+    cfg = preset("tiny")
+    sd = random_hf_state_dict(cfg)
+    q = "int8d:qkv+gu|sq|lastbf16|fqkv|fmlp"
+    w = prepare_mk_weights(sd, cfg.as_mk_cfg(), q, 2048, log=lambda *a: None)
+    args = (w, sd["model.embed_tokens.weight"], sd["model.norm.weight"], cfg, q, sd["lm_head.weight"])
+    ids = random_token_ids(2, 512)
+    _, lv = emulate.mk_forward(ids, *args, attn="v2")
+    _, la = emulate.mk_forward(ids, *args, attn="auto")
+    fx = np.load(os.path.join(os.path.dirname(__file__), "golden", "golden_tiny_b2_s512.npz"))
+    gold = torch.from_numpy(fx["logits"])
+    assert not torch.equal(lv, la)
+    for lg in (lv, la):
+        assert (lg - gold).abs().max() < 0.05
+        assert torch.equal(lg.argmax(-1), gold.argmax(-1))
+    ids = random_token_ids(1, 2048)
+    _, lv = emulate.mk_forward(ids, *args, attn="v2")
+    _, la = emulate.mk_forward(ids, *args, attn="auto")
+    assert torch.equal(lv, la)
+
+
 # ---------------------------------------------------------------------------------------- fp8 / static modes
 def _e4m3_table():
     """(code, value) of every finite float8_e4m3fn code from the format's definition: sign, 4 exponent bits
