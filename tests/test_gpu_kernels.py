@@ -284,14 +284,16 @@ def test_gemm_residual_epilogues():
 
 
 def test_gate_up_silu_epilogue():
-    """fused_mlp gate/up (mk_mlp.py:79-84): packed 32-interleave, h = silu(g) * u."""
+    """fused_mlp gate/up (mk_mlp.py:79-84): packed in [32 gate | 32 up] blocks, h = silu(g) * u.  One
+    8192-row launch (256x128 tiles) vs the oracle on its first and last 640 rows, and 100- and 640-row
+    launches (64x128 and 256x128 tiles) equal to its first rows, bit for bit."""
     from minicpm5_mk import ops
     from minicpm5_mk.mk_weights import interleave_gu, mlp_chunk
     from oracle import emulate
 
     dev = _dev()
     g = torch.Generator().manual_seed(21)
-    T, H, inter = 640, 1536, 4608
+    T, H, inter = 8192, 1536, 4608
     x = torch.randn(T, H, generator=g).to(BF16)
     w = torch.randint(-127, 128, (H, 2, inter), generator=g, dtype=torch.int8)
     s = torch.rand(2, inter, generator=g) * 2e-3
@@ -299,15 +301,16 @@ def test_gate_up_silu_epilogue():
     ic = mlp_chunk(inter)
     w_il, s_il = interleave_gu(w, s, ic)                       # reference layout (H, 2I), (1, 2I)
     wp = ops.pack_weight(w_il.to(dev), map_gu=True, ic=ic, inter=inter)     # (2I, H) packed
-    # scales in packed order: row p <- reference column map(p)
-    p = torch.arange(2 * inter)
-    blk, half, n = p // 64, (p // 32) % 2, (p // 64) * 32 + p % 32
-    src = (n // ic) * 2 * ic + half * ic + n % ic
-    s_p = s_il.reshape(-1)[src].contiguous()
+    s_p = _pack_gu_scales(s_il, inter).to(dev)
     q, sx = ops.row_quant(x.to(dev), a.to(dev), 1e-6, True, True)
-    h = ops.gemm(q, wp, "dq_silu", rs=sx, cs=s_p.to(dev)).float().cpu()
-    qr, sxr = emulate.row_quant(x.float(), a, 1e-6, True, True)
-    gu = (emulate.int_matmul(qr, w.reshape(H, -1)).float() * sx.cpu()[:, None]) * s.reshape(1, -1)
+    h = ops.gemm(q, wp, "dq_silu", rs=sx, cs=s_p)
+    for M in (100, 640):
+        hm = ops.gemm(q[:M].contiguous(), wp, "dq_silu", rs=sx[:M].contiguous(), cs=s_p)
+        assert torch.equal(hm, h[:M]), M
+    rows = torch.cat([torch.arange(640), torch.arange(T - 640, T)])
+    h = h.float().cpu()[rows]
+    qr, _ = emulate.row_quant(x[rows].float(), a, 1e-6, True, True)
+    gu = (emulate.int_matmul(qr, w.reshape(H, -1)).float() * sx.cpu()[rows][:, None]) * s.reshape(1, -1)
     ref = emulate.silu_f32(gu[:, :inter]) * gu[:, inter:]
     err = (h - ref).abs()
     assert (err <= ref.abs() * 2.0 ** -7 + 1e-6).all(), float(err.max())
@@ -327,7 +330,8 @@ def test_lm_head():
 
 
 def _pack_gu_scales(s_il, inter):
-    """Per-column scales of the chunk-interleaved gate/up matrix in the packed 32-column [gate | up] order."""
+    """Per-column scales of the chunk-interleaved gate/up matrix in the packed order: packed row p holds
+    [32 gate | 32 up] block p // 64, half (p // 32) % 2, intermediate column 32 (p // 64) + p % 32."""
     from minicpm5_mk.mk_weights import mlp_chunk
 
     ic = mlp_chunk(inter)
