@@ -8,7 +8,8 @@
     tests/golden/make_golden.py from oracle/golden.py).  The argmax must be identical (tie-aware for the
     one config whose golden top-2 margin is below the W8A8 error); the logits tolerance is stated per
     config below (about 2x the CPU emulator's own W8A8 error vs FP32).
-  * MiniCPM5-1B at (1, 1024) (the short-prompt path) vs its FP32 golden, same checks.
+  * full architectures at (1, 1024) (the short-prompt path) vs their FP32 goldens, bounds and argmax
+    rules from the CPU emulation of the same numerics.
   * full architectures at (1, 8192): libmk vs full-size fixtures of the CPU emulation of the same W8A8
     numerics (tests/golden/emulate_*.npz, tests/golden/make_emulator_fixture.py), bounded tightly.
   * batch invariance at the reference's batch shapes (B, 8192), B = 4..32 for 1B-hd96 and 2B (the
@@ -257,7 +258,9 @@ def _golden_checks(name, lg, g, tol_max, tol_mean, strict):
     print(f"[full] {name}: logits max {err.max():.4f} mean {err.mean():.4f} rel {err.max() / g.abs().max():.4f}; "
           f"argmax {int(lg.argmax())} vs {int(g.argmax())} (golden margin {float(srt[0] - srt[1]):.4f}); "
           f"mean |dlogprob| top20 {float(dlp):.4f}", flush=True)
-    if strict:
+    if isinstance(strict, (tuple, frozenset, set)):   # the golden top-1 or these named tokens
+        assert int(lg.argmax()) in {int(g.argmax()), *strict}
+    elif strict:
         assert int(lg.argmax()) == int(g.argmax())
     else:
         assert float(lpg.max() - lpg[int(lg.argmax())]) <= 0.1
@@ -277,23 +280,33 @@ def test_full_model_vs_fp32_golden(name, tol_max, tol_mean, strict):
     _golden_checks(name, lg.cpu()[0], torch.from_numpy(gold["logits"][0]), tol_max, tol_mean, strict)
 
 
-def test_full_model_short_prompt_vs_fp32_golden():
-    """MiniCPM5-1B at (1, 1024) -- the short-prompt path: 64x128 two-stage GEMM tiles, one attention
-    workgroup per work item, the attention launch's weight prefetch -- vs the FP32 golden
-    tests/golden/golden_1b_b1_s1024.npz (make_golden.py --preset 1b --seq 1024; top-1 margin 0.14).  The
-    CPU emulation of the same W8A8 numerics errs max 0.202 / mean 0.035 there (with the reference's own
-    S <= 1024 attention kernel, emulate.mk_forward(attn="auto"): 0.188 / 0.035), as at (1, 8192), so the
-    1B bounds of that test apply, with the strict argmax."""
+# (preset, max, mean, argmax rule) at (1, 1024) against tests/golden/golden_<preset>_b1_s1024.npz.  The CPU
+# emulation of the same W8A8 numerics (v2 attention / the reference's own S <= 1024 kernel) errs:
+#   1b       max 0.202 / 0.188  mean 0.035 / 0.035   argmax = golden top-1 (margin 0.140)
+#   1b-hd96  max 0.218 / 0.205  mean 0.042 / 0.039   top-1, or golden #2 (token 123131, 0.039 nats below),
+#                                                    which the v2 emulation picks
+#   2b       max 0.594 / 0.528  mean 0.092 / 0.095   golden #2 (token 43840, 0.183 nats below) under both
+#                                                    attention kernels: the W8A8 error moves the argmax
+# Bounds: 1b and 1b-hd96 those of (1, 8192); 2b max 1.2 (2x the emulation), mean 0.19.
+SHORT = [("1b", 0.45, 0.075, True), ("1b-hd96", 0.55, 0.095, (123131,)), ("2b", 1.2, 0.19, (43840,))]
+
+
+@pytest.mark.parametrize("name,tol_max,tol_mean,rule", SHORT)
+def test_full_model_short_prompt_vs_fp32_golden(name, tol_max, tol_mean, rule):
+    """Full architectures at (1, 1024) -- the short-prompt path: 64x128 two-stage GEMM tiles, one
+    attention workgroup per work item, the attention launch's weight prefetch -- vs their FP32 goldens
+    (make_golden.py --seq 1024).  Bounds and argmax rules from the CPU emulation of the same numerics
+    (table above): where that emulation itself picks the golden's #2 token, so may the GPU."""
     from minicpm5_mk.synth import random_token_ids
 
-    gold = np.load(os.path.join(HERE, "golden", "golden_1b_b1_s1024.npz"))
+    gold = np.load(os.path.join(HERE, "golden", f"golden_{name}_b1_s1024.npz"))
     meta = json.loads(str(gold["meta"]))
-    assert meta["seq"] == 1024 and meta["weight_seed"] == _golden("1b")[1]["weight_seed"]
-    m = _full_model("1b")
+    assert meta["seq"] == 1024 and meta["weight_seed"] == _golden(name)[1]["weight_seed"]
+    m = _full_model(name)
     ids = random_token_ids(1, 1024, seed=meta["id_seed"])
-    print("[full] 1b (1, 1024) forward", flush=True)
+    print(f"[full] {name} (1, 1024) forward", flush=True)
     _, lg = m.forward(ids.reshape(-1).to(_dev()), 1, 1024, logits=True)
-    _golden_checks("1b-s1024", lg.cpu()[0], torch.from_numpy(gold["logits"][0]), 0.45, 0.075, True)
+    _golden_checks(f"{name}-s1024", lg.cpu()[0], torch.from_numpy(gold["logits"][0]), tol_max, tol_mean, rule)
 
 
 # GPU vs the CPU emulation of the same W8A8 numerics at (1, 8192): (preset, max-abs bound, mean-abs bound).
