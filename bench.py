@@ -17,10 +17,13 @@ Extra fields:
   kernels       the same for every kernel category: QKV / gate-up GEMMs (int8 MFMA, peak 5.0 POP/s when
                 quantised), O / down (bf16 unless quantised), the row kernels and the LM head (HBM GB/s).
   cpu_baseline  the oracle's FP32 CPU forward (oracle/golden.py, a restatement of the reference's
-                FP32 golden) of one whole 8192-token sequence of the main architecture with every host
-                thread: one warm-up of the first layer, then --cpu-runs timed full forwards (median).
+                FP32 golden) of --cpu-batch whole 8192-token sequences (default 1) of the main
+                architecture with every host thread: one warm-up of the first layer, then --cpu-runs
+                timed runs (median).  `per_batch` gives tokens/s and ms at B = 1..32: the timed batch,
+                and the others as a linear extrapolation from it, labelled as such (the FP32 path runs
+                one sequence at a time, as the reference's golden does).
   sweep         the metric's other points: tokens/s, mean and p50 latency at (B, 8192) for each
-                (architecture, B) of --sweep (default: 1B at B = 4..32, 2B at B = 1..32, 1B-hd96 at B = 1),
+                (architecture, B) of --sweep (default: 1B at B = 4..32, 2B and 1B-hd96 at B = 1..32),
                 each with `roofline_ms`, the whole model's bound at MI355X's published peaks (every linear
                 at its operand type's dense MFMA peak, causal attention at the bf16 peak, the LM head's
                 weight read at HBM bandwidth), and `frac_roofline` = roofline_ms / mean latency.
@@ -43,7 +46,7 @@ METRIC = "prefill tokens/sec at (B,8192) B=1..32, 1B and 2B arch; p50 ms at (1,8
 # 256 MiB copy's counters) for the default workload; (arch, B, S, quant) -> (bytes, source file)
 ATTN_TRAFFIC = {("1b", 1, 8192, "auto"): (77.0e6 + 33.6e6, "profiles/mfma_util_hbm_1b_b1_s8192.txt"),
                 ("2b", 1, 8192, "auto"): (77.1e6 + 33.6e6, "profiles/mfma_util_hbm_2b_b1_s8192.txt")}
-DEFAULT_SWEEP = "1b:4,8,16,32;2b:1,4,8,16,32;1b-hd96:1"
+DEFAULT_SWEEP = "1b:4,8,16,32;2b:1,4,8,16,32;1b-hd96:1,4,8,16,32"
 
 
 def log(*a):
@@ -235,10 +238,11 @@ def attainable_peaks(iters=3000):
     return out
 
 
-def cpu_baseline(cfg, runs, seq=8192):
-    """The oracle's FP32 forward (restating benchmark/f32_golden.py) of one whole `seq`-token sequence
-    with every host thread: one untimed warm-up over the first layer, then `runs` timed full forwards
-    (embedding, all L layers, final norm, LM head); value = seq / median time."""
+def cpu_baseline(cfg, runs, seq=8192, batch=1):
+    """The oracle's FP32 forward (restating benchmark/f32_golden.py) of `batch` whole `seq`-token
+    sequences, one after another, with every host thread: one untimed warm-up over the first layer, then
+    `runs` timed runs (embedding, all L layers, final norm, LM head per sequence); value =
+    batch * seq / median time."""
     import torch
 
     from minicpm5_mk.synth import random_hf_state_dict, random_token_ids
@@ -248,21 +252,29 @@ def cpu_baseline(cfg, runs, seq=8192):
     t0 = time.perf_counter()
     W = golden.load_f32(random_hf_state_dict(cfg), cfg)
     t_load = time.perf_counter() - t0
-    ids = random_token_ids(1, seq)[0]
+    ids = random_token_ids(batch, seq)
     cos, sin = golden.rope_tables(seq, cfg.head_dim, cfg.rope_theta)
-    golden.forward_one(ids, W, cfg.replace(num_layers=1), cos, sin)      # warm-up: one layer
+    golden.forward_one(ids[0], W, cfg.replace(num_layers=1), cos, sin)      # warm-up: one layer
     times = []
     for _ in range(runs):
         t0 = time.perf_counter()
-        golden.forward_one(ids, W, cfg, cos, sin)
+        for b in range(batch):
+            golden.forward_one(ids[b], W, cfg, cos, sin)
         times.append(time.perf_counter() - t0)
     med = pctl(times, 50)
-    return {"value": round(seq / med, 1), "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"oracle FP32 forward (oracle/golden.py) of one whole {seq}-token sequence of {cfg.name} "
-                      f"({cfg.num_layers} layers + final norm + LM head), {runs} timed runs after a one-layer "
+    tps = batch * seq / med
+    per_batch = []
+    for b in sorted({1, 4, 8, 16, 32, batch}):
+        per_batch.append({"batch": b, "tokens_per_s": round(tps, 1), "p50_ms": round(med * 1e3 * b / batch, 1),
+                          "timed": b == batch,
+                          **({} if b == batch else {"extrapolated_from_batch": batch})})
+    what = "one whole" if batch == 1 else f"{batch} whole"
+    return {"value": round(tps, 1), "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"oracle FP32 forward (oracle/golden.py) of {what} {seq}-token sequence(s) of {cfg.name} "
+                      f"({cfg.num_layers} layers + final norm + LM head each), {runs} timed runs after a one-layer "
                       f"warm-up: {', '.join(f'{t:.1f}' for t in times)} s (median {med:.1f} s); weights "
                       f"generated and upcast in {t_load:.1f} s (untimed)",
-            "cpu_model": _cpu_model()}
+            "batch": batch, "per_batch": per_batch, "cpu_model": _cpu_model()}
 
 
 def _cpu_model():
@@ -289,6 +301,7 @@ def main():
                     help="extra (architecture, batch) rows: 'arch:B,B;arch:B' ('B,B' = the --arch architecture; "
                          "'' = none)")
     ap.add_argument("--cpu-runs", type=int, default=2, help="timed full CPU forwards of the baseline (0 = skip)")
+    ap.add_argument("--cpu-batch", type=int, default=1, help="sequences per timed CPU baseline run")
     ap.add_argument("--no-kernels", action="store_true")
     ap.add_argument("--kernels-only", action="store_true",
                     help="only the per-kernel timing loops + a 256 MiB device copy (rocprofv3 --pmc calibration)")
@@ -368,7 +381,7 @@ def main():
     eng.close()
     del eng
     torch.cuda.empty_cache()
-    cpu = cpu_baseline(cfg, args.cpu_runs, args.seq) if args.cpu_runs > 0 else None
+    cpu = cpu_baseline(cfg, args.cpu_runs, args.seq, args.cpu_batch) if args.cpu_runs > 0 else None
     if cpu:
         log(f"[bench] cpu baseline: {cpu}")
 

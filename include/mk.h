@@ -128,7 +128,10 @@ int mk_precompile(mk_model* m, const int32_t* input_ids, int bs, int seq, void* 
  * cached graphs when it changes. */
 int mk_set_attn_prep_fused(mk_model* m, int enable);
 
-/* Number of hipGraphs the model holds (at most 16: the least recently captured is dropped first). */
+/* Number of hipGraphs the model holds (at most 16: the least recently captured is dropped first).
+ * A cached graph is destroyed (eviction, mk_set_attn_prep_fused / mk_set_max_chunk changes,
+ * mk_model_destroy) only after its latest replay has finished: each replay records an event on the
+ * caller's stream, and the destroy waits for that event (the host blocks until then). */
 int mk_graph_count(const mk_model* m, int* n);
 
 /* 1 (default) replays captured hipGraphs, 0 launches kernels eagerly on every call. */
@@ -238,9 +241,10 @@ int mk_act_quant(const void* x, int x_f32, const float* a, int T, int H, float e
 #define MK_IN_INT8 1
 #define MK_IN_FP8 2
 /* MFMA GEMM with a fused epilogue; in_type is MK_IN_*.  A and B 16-byte aligned, lda / ldb >= K in
- * elements (16-byte multiples), K a multiple of 32 bytes, and each operand spanning < 4 GiB (M lda and
- * N ldb bytes: 32-bit load offsets); else MK_EINVAL.  Results do not depend on the tile shape the
- * launcher picks for (M, N, K). */
+ * elements (16-byte multiples), K a multiple of 64 bytes (32 bytes suffice for M <= 32, which runs the
+ * weight-streaming kernel; the SiLU epilogues always take the tiled kernels), and each operand spanning
+ * < 4 GiB (M lda and N ldb bytes: 32-bit load offsets); else MK_EINVAL.  Results do not depend on the
+ * tile shape the launcher picks for (M, N, K). */
 int mk_gemm(int in_type, int epi, const void* A, int lda, const void* B, int ldb, int M, int N, int K,
             void* out, int ldo, void* res, int ldr, const float* rs, const float* cs, const float* aux,
             void* stream);

@@ -134,8 +134,7 @@ int mk_precompile(mk_model* m, const int32_t* input_ids, int bs, int seq, void* 
 int mk_set_attn_prep_fused(mk_model* m, int enable) {
   MK_REQUIRE(m != nullptr, "set_attn_prep_fused: null model");
   if (m->impl->fuse_prep != (enable != 0)) {   // captured graphs hold the old launch sequence
-    for (auto& g : m->impl->graphs) hipGraphExecDestroy(g.exec);
-    m->impl->graphs.clear();
+    m->impl->drop_graphs();   // each after its latest replay has finished
   }
   m->impl->fuse_prep = enable != 0;
   return MK_OK;
@@ -157,8 +156,7 @@ int mk_set_max_chunk(mk_model* m, int seqs) {
   MK_REQUIRE(m != nullptr, "set_max_chunk: null model");
   MK_REQUIRE(seqs >= 0, "set_max_chunk: seqs must be >= 0");
   if (m->impl->max_chunk != seqs) {   // captured graphs hold the old chunking
-    for (auto& g : m->impl->graphs) hipGraphExecDestroy(g.exec);
-    m->impl->graphs.clear();
+    m->impl->drop_graphs();   // each after its latest replay has finished
   }
   m->impl->max_chunk = seqs;
   return MK_OK;

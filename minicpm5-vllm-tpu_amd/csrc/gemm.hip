@@ -971,8 +971,9 @@ void launch_t(const GemmArgs& g, hipStream_t st) {
     case 1: launch_c<CfgL, IN, EPI>(g, st); break;
     case 3: launch_c<CfgS, IN, EPI>(g, st); break;
     case 4: launch_c<CfgX, IN, EPI>(g, st); break;
-    case 5:
+    case 5:   // 96-column waves cannot hold whole [gate | up] blocks: SiLU epilogues take the 256x128 tile
       if constexpr (!silu) launch_c<CfgN, IN, EPI>(g, st);
+      else launch_c<CfgM, IN, EPI>(g, st);
       break;
     case 6: launch_c<CfgD, IN, EPI>(g, st); break;
     case 7: launch_c<CfgE, IN, EPI>(g, st); break;

@@ -5,9 +5,10 @@
 // sequence of HIP kernel launches on one stream, captured once per (bs, seq, buffers) into a
 // hipGraph (the reference caches one compiled program per static-argument set, model.py:54-86).
 //
-// Differences by design (one GPU, 288 GB HBM): no microbatch chunking (the reference splits B > 4
-// into 4 x 8192-token chunks to bound TPU HBM, mk_jax.py:572-605; here the activations of
-// B = 32 x 8192 tokens take ~6 GB); weights are repacked once to K-contiguous rows.
+// Differences by design (one GPU, 288 GB HBM): batches are chunked only as far as the 32-bit GEMM
+// operand offsets need (chunk_seqs: every operand of a chunk spans < 4 GiB, e.g. 42 x 8192 tokens for
+// MiniCPM5-2B with a bf16 down projection), not into the reference's 4 x 8192-token chunks that bound
+// TPU HBM (mk_jax.py:572-605); weights are repacked once to K-contiguous rows.
 #include <math.h>
 
 #include <algorithm>
@@ -314,8 +315,23 @@ int model_create(const mk_config* cfg, const char* quant, const mk_weights* w, v
   return MK_OK;
 }
 
+void destroy_graph(CachedGraph& g) {
+  if (g.done) {
+    hipEventSynchronize(g.done);
+    hipEventDestroy(g.done);
+    g.done = nullptr;
+  }
+  if (g.exec) hipGraphExecDestroy(g.exec);
+  g.exec = nullptr;
+}
+
+void Model::drop_graphs() {
+  for (auto& g : graphs) destroy_graph(g);
+  graphs.clear();
+}
+
 Model::~Model() {
-  for (auto& g : graphs) hipGraphExecDestroy(g.exec);
+  drop_graphs();
   if (cap_stream) hipStreamDestroy(cap_stream);
 }
 
@@ -798,10 +814,10 @@ int check_run(const Model* m, const int32_t* ids, int bs, int seq, const void* h
 
 // The cached graph of `key`, captured (launches recorded on the model's private capture stream, nothing
 // executed) and instantiated on first use.  The cache keeps the kMaxGraphs most recently captured shapes.
-int graph_for(Model* m, const GraphKey& key, const WorkLayout& W, hipGraphExec_t* out) {
+int graph_for(Model* m, const GraphKey& key, const WorkLayout& W, CachedGraph** out) {
   for (auto& g : m->graphs) {
     if (g.key == key) {
-      *out = g.exec;
+      *out = &g;
       return MK_OK;
     }
   }
@@ -827,12 +843,19 @@ int graph_for(Model* m, const GraphKey& key, const WorkLayout& W, hipGraphExec_t
     set_error(std::string("forward: graph instantiate failed: ") + hipGetErrorString(e));
     return MK_EHIP;
   }
-  if (m->graphs.size() >= Model::kMaxGraphs) {
-    hipGraphExecDestroy(m->graphs.front().exec);
+  hipEvent_t done = nullptr;
+  e = hipEventCreateWithFlags(&done, hipEventDisableTiming);
+  if (e != hipSuccess) {
+    hipGraphExecDestroy(exec);
+    set_error(std::string("forward: event create failed: ") + hipGetErrorString(e));
+    return MK_EHIP;
+  }
+  if (m->graphs.size() >= Model::kMaxGraphs) {   // least recently captured shape out (after its last replay)
+    destroy_graph(m->graphs.front());
     m->graphs.erase(m->graphs.begin());
   }
-  m->graphs.push_back({key, exec});
-  *out = exec;
+  m->graphs.push_back({key, exec, done});
+  *out = &m->graphs.back();
   return MK_OK;
 }
 
@@ -846,10 +869,11 @@ int model_forward(Model* m, const int32_t* ids, int bs, int seq, void* hidden, f
   if (!m->use_graph)
     return launch_batches(*m, ids, bs, seq, static_cast<uint16_t*>(hidden), logits, static_cast<char*>(ws), W,
                           nullptr, st);
-  hipGraphExec_t exec = nullptr;
-  rc = graph_for(m, GraphKey{bs, seq, ids, hidden, logits, ws}, W, &exec);
+  CachedGraph* g = nullptr;
+  rc = graph_for(m, GraphKey{bs, seq, ids, hidden, logits, ws}, W, &g);
   if (rc) return rc;
-  MK_HIP_CHECK(hipGraphLaunch(exec, st));
+  MK_HIP_CHECK(hipGraphLaunch(g->exec, st));
+  MK_HIP_CHECK(hipEventRecord(g->done, st));
   return MK_OK;
 }
 
@@ -858,8 +882,8 @@ int model_precompile(Model* m, const int32_t* ids, int bs, int seq, void* hidden
   WorkLayout W{};
   int rc = check_run(m, ids, bs, seq, hidden, logits, ws, ws_bytes, &W, "precompile");
   if (rc) return rc;
-  hipGraphExec_t exec = nullptr;
-  return graph_for(m, GraphKey{bs, seq, ids, hidden, logits, ws}, W, &exec);
+  CachedGraph* g = nullptr;
+  return graph_for(m, GraphKey{bs, seq, ids, hidden, logits, ws}, W, &g);
 }
 
 }  // namespace mk

@@ -39,10 +39,16 @@ struct GraphKey {
   }
 };
 
+// A captured forward and an event recorded on the caller's stream after its latest replay: the exec is
+// destroyed only once that event has completed (HIP does not promise deferred destruction of a graph
+// that is still running).
 struct CachedGraph {
   GraphKey key;
   hipGraphExec_t exec;
+  hipEvent_t done;
 };
+// Waits for the graph's latest replay, then destroys it.
+void destroy_graph(CachedGraph& g);
 
 struct Model {
   static constexpr size_t kMaxGraphs = 16;
@@ -56,6 +62,7 @@ struct Model {
   bool fuse_prep = true;   // K RoPE / V^T written by the QKV projection's epilogue (else the prep kernel)
   hipStream_t cap_stream = nullptr;
   std::vector<CachedGraph> graphs;
+  void drop_graphs();   // destroy_graph on every cached graph
   ~Model();
 };
 

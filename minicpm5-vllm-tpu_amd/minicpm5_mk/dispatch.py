@@ -119,22 +119,32 @@ def step_view_from_runner(runner, scheduler_output) -> StepView:
     )
 
 
+# What the installed hook checks against: the most recent install's model length and max_tokens rule.
+# The wrapper reads this slot on every step, so a model built after an earlier one was freed (same
+# process, same runner class) re-points the hook instead of inheriting the first model's length.
+_HOOK_CFG = {"max_seq_of": lambda runner: 0, "require_mt1": True}
+
+
 def install_runner_hook(runner_cls, max_seq_of, require_mt1: bool = True) -> bool:
     """Wrap `runner_cls._prepare_inputs` (and `_dummy_run` when present) so each step records its
-    decision in STATE.  `max_seq_of(runner)` gives the model's max length.  Idempotent; returns False
-    when the class has no `_prepare_inputs`."""
+    decision in STATE.  `max_seq_of(runner)` gives the model's max length.  The class is wrapped once;
+    every call updates what the wrapper checks against.  Returns False when the class has no
+    `_prepare_inputs`."""
     if getattr(runner_cls, "_minicpm5_mk_hooked", False):
+        _HOOK_CFG.update(max_seq_of=max_seq_of, require_mt1=require_mt1)
         return True
     orig_prepare = getattr(runner_cls, "_prepare_inputs", None)
     if orig_prepare is None:
         return False
+    _HOOK_CFG.update(max_seq_of=max_seq_of, require_mt1=require_mt1)
 
     @functools.wraps(orig_prepare)
     def _prepare_inputs(self, scheduler_output, *args, **kwargs):
         STATE.set(None, "init")
         out = orig_prepare(self, scheduler_output, *args, **kwargs)
         try:
-            batch, reason = eligible_step(step_view_from_runner(self, scheduler_output), max_seq_of(self), require_mt1)
+            batch, reason = eligible_step(step_view_from_runner(self, scheduler_output),
+                                          _HOOK_CFG["max_seq_of"](self), _HOOK_CFG["require_mt1"])
         except Exception as e:  # noqa: BLE001  (a runner layout this hook does not know: stock path)
             batch, reason = None, f"check_error:{type(e).__name__}"
         STATE.set(batch, reason)

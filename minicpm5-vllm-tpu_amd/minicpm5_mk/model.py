@@ -17,10 +17,23 @@ Without the reference's hidden-state selection patch (model.py:224-235) the forw
 tensor with the B final-normed last-token rows at rows b*S + S - 1, the rows the stock logits
 selection reads.
 
+Megakernel-only mode (MINICPM5_MK_FREE_STOCK=1, model.py:683-705, :787-794): after the build the stock
+decoder-layer weights are dropped; a dummy (profiling) run then returns zeros and any other ineligible
+step raises instead of running stock attention.  Only in this mode may the engine skip KV-cache
+allocation for fast-path requests (the hook in `minicpm5_mk.register`), because no stock forward can
+then read the unwritten KV blocks.
+
+Prefix caching: a fast-path prefill writes no KV cache, but vLLM registers the request's full prompt
+blocks in its prefix-cache table before the forward runs; a later request sharing that prefix would
+hit those blocks and the stock path would attend over KV that was never written.  The fast path is
+therefore off when the engine runs with prefix caching (the reference runs only with it off,
+benchmark/run_benchmark.py:43), and megakernel-only mode refuses to start with it.
+
 Requires vLLM (imported at module import, like the reference).  Environment knobs kept from the
 reference (model.py:23-32): MINICPM5_MK_ENABLE, MINICPM5_MK_QUANT, MINICPM5_MK_ATTN,
-MINICPM5_MK_REQUIRE_MAX_TOKENS_1, MINICPM5_MK_FREE_STOCK, MINICPM5_MK_STATUS_DIR, MINICPM5_MK_PRECOMPILE; and
-MINICPM5_MK_CHECK_POSITIONS=1 cross-checks each fast-path step against the device positions (syncs).
+MINICPM5_MK_REQUIRE_MAX_TOKENS_1, MINICPM5_MK_FREE_STOCK, MINICPM5_MK_STATUS_DIR, MINICPM5_MK_PRECOMPILE,
+MINICPM5_MK_LOG_EVERY (log the path counters every N forwards); and MINICPM5_MK_CHECK_POSITIONS=1
+cross-checks each fast-path step against the device positions (syncs).
 """
 from __future__ import annotations
 
@@ -50,7 +63,8 @@ _WEIGHT_SUFFIXES = (
 
 
 def _hook_vllm_runner(model) -> bool:
-    """Install the eligibility hook on vLLM's v1 GPU model runner (one class per process)."""
+    """Install the eligibility hook on vLLM's v1 GPU model runner (one class per process); a later
+    model instance re-points the hook at itself."""
     try:
         from vllm.v1.worker.gpu_model_runner import GPUModelRunner
     except ImportError:
@@ -58,6 +72,10 @@ def _hook_vllm_runner(model) -> bool:
     ref = weakref.ref(model)
     require_mt1 = os.environ.get("MINICPM5_MK_REQUIRE_MAX_TOKENS_1", "1") != "0"
     return install_runner_hook(GPUModelRunner, lambda runner: ref()._mk_max_seq if ref() else 0, require_mt1)
+
+
+def _free_stock() -> bool:
+    return os.environ.get("MINICPM5_MK_FREE_STOCK", "0") == "1"
 
 
 class MiniCPM5MegakernelForCausalLM(LlamaForCausalLM):
@@ -69,8 +87,18 @@ class MiniCPM5MegakernelForCausalLM(LlamaForCausalLM):
         self._mk_max_seq = int(vllm_config.model_config.max_model_len)
         self._mk_attn = os.environ.get("MINICPM5_MK_ATTN", "auto")
         self._mk_counts = {"mk": 0, "stock": 0}
+        self._mk_log_every = int(os.environ.get("MINICPM5_MK_LOG_EVERY", "0") or 0)
         self._mk_model = None
         self._mk_status = None
+        self._mk_stock_freed = False
+        cache_cfg = getattr(vllm_config, "cache_config", None)
+        if self._mk_enabled and getattr(cache_cfg, "enable_prefix_caching", False):
+            if _free_stock():
+                raise RuntimeError("minicpm5_mk: MINICPM5_MK_FREE_STOCK=1 needs the fast path, which does not run with "
+                                   "prefix caching (its prefills write no KV cache); start the engine with "
+                                   "enable_prefix_caching=False")
+            logger.warning("minicpm5_mk: prefix caching is on; fast path disabled (its prefills write no KV cache)")
+            self._mk_enabled = False
         rope = getattr(hf, "rope_scaling", None) or getattr(hf, "rope_parameters", None)
         if isinstance(rope, dict) and rope.get("rope_type", rope.get("type", "default")) not in (None, "default"):
             logger.warning("minicpm5_mk: rope_scaling=%s unsupported; fast path disabled", rope)
@@ -103,7 +131,7 @@ class MiniCPM5MegakernelForCausalLM(LlamaForCausalLM):
         try:
             self._mk_build(stash)
         except Exception:
-            if os.environ.get("MINICPM5_MK_FREE_STOCK", "0") == "1":
+            if _free_stock():
                 logger.exception("minicpm5_mk: build failed and MINICPM5_MK_FREE_STOCK=1")
                 raise
             logger.exception("minicpm5_mk: build failed; stock path only")
@@ -123,23 +151,45 @@ class MiniCPM5MegakernelForCausalLM(LlamaForCausalLM):
         self._mk_model = MkModel(self._mk_keep, embed, w["cos"].to(dev), w["sin"].to(dev),
                                  stash["model.norm.weight"].to(torch.bfloat16).to(dev), quant, c.n_q, c.n_kv,
                                  c.head_dim, c.eps)
-        self._mk_status = {"arch": "MiniCPM5MegakernelForCausalLM", "quant": quant, "attn": self._mk_attn,
-                           "backend": "libmk (HIP, gfx950)", "shapes": {}}
-        self._mk_write_status()
         logger.info("minicpm5_mk: libmk ready (quant=%s) in %.1fs", quant, time.perf_counter() - t0)
+        if _free_stock():
+            self._mk_free_stock_layers()
+        # the reference's status keys (model.py:683-689); one GPU per model: tp 1, rank 0, no multicore modes
+        self._mk_status = {"arch": "MiniCPM5MegakernelForCausalLM", "tp": 1, "rank": 0, "quant": quant,
+                           "quant_tp": quant, "attn": self._mk_attn, "multicore_modes": [],
+                           "stock_freed": self._mk_stock_freed, "backend": "libmk (HIP, gfx950)", "shapes": {}}
+        self._mk_write_status()
         # hipGraphs of the listed shapes captured now instead of at each shape's first step (model.py:690-698)
         self._mk_model.precompile(parse_precompile(os.environ.get("MINICPM5_MK_PRECOMPILE", "")), logits=False,
                                   log=logger.info)
 
+    def _mk_free_stock_layers(self) -> None:
+        """Drop the stock decoder layers' weights (model.py:700-705): megakernel-only from here on."""
+        for layer in self.model.layers:
+            for p in layer.parameters():
+                p.data = torch.empty((0,), dtype=p.dtype, device=p.device)
+        self._mk_stock_freed = True
+        logger.info("minicpm5_mk: freed stock decoder-layer weights (no stock fallback)")
+
     def _mk_write_status(self) -> None:
+        """The path record (one small JSON; first use of each shape and each stock reason only)."""
         d = os.environ.get("MINICPM5_MK_STATUS_DIR")
         if not d or self._mk_status is None:
             return
-        os.makedirs(d, exist_ok=True)
-        path = os.path.join(d, "minicpm5_mk_status_rank0.json")
-        with open(path + ".tmp", "w") as f:
-            json.dump(self._mk_status, f, indent=1)
-        os.replace(path + ".tmp", path)
+        try:
+            os.makedirs(d, exist_ok=True)
+            path = os.path.join(d, "minicpm5_mk_status_rank0.json")
+            with open(path + ".tmp", "w") as f:
+                json.dump(self._mk_status, f, indent=1)
+            os.replace(path + ".tmp", path)
+        except OSError as e:
+            logger.warning("minicpm5_mk: could not write status file: %r", e)
+
+    def _mk_maybe_log(self, msg: str, reason: str) -> None:
+        """Every MINICPM5_MK_LOG_EVERY forwards: the path counters (model.py:797-801)."""
+        n = self._mk_log_every
+        if n and (self._mk_counts["mk"] + self._mk_counts["stock"]) % n == 0:
+            logger.info("minicpm5_mk: %s counts=%s last_reason=%s", msg, self._mk_counts, reason)
 
     def forward(self, input_ids, positions, intermediate_tensors=None, inputs_embeds=None):
         batch, reason = STATE.take()
@@ -155,9 +205,25 @@ class MiniCPM5MegakernelForCausalLM(LlamaForCausalLM):
                 self._mk_status["shapes"][key] = {"mode": "single", "quant": self._mk_model.quant}
                 self._mk_write_status()
             self._mk_counts[key] += 1
+            self._mk_maybe_log(f"mk bs={B} seq={S} T={input_ids.numel()}", reason)
             rows = self._mk_model.forward(input_ids.reshape(-1)[: B * S].to(torch.int32), B, S)
             return scatter_last_rows(rows, B, S, input_ids.numel())
         self._mk_counts["stock"] += 1
         rkey = f"stock:{reason}"
-        self._mk_counts[rkey] = self._mk_counts.get(rkey, 0) + 1
+        if rkey not in self._mk_counts:
+            self._mk_counts[rkey] = 0
+            if reason != "dummy":
+                logger.info("minicpm5_mk: stock path (reason=%s, T=%d)", reason,
+                            input_ids.numel() if input_ids is not None else -1)
+                if self._mk_status is not None:
+                    self._mk_status.setdefault("stock_reasons", []).append(reason)
+                    self._mk_write_status()
+        self._mk_counts[rkey] += 1
+        self._mk_maybe_log(f"stock T={input_ids.numel() if input_ids is not None else -1}", reason)
+        if self._mk_stock_freed:
+            if reason == "dummy":
+                src = input_ids if input_ids is not None else inputs_embeds
+                n = src.numel() if input_ids is not None else src.shape[0]
+                return torch.zeros((n, self._mk_cfg.hidden), dtype=torch.bfloat16, device=src.device)
+            raise RuntimeError(f"minicpm5_mk: stock path needed ({reason}) but stock weights were freed")
         return super().forward(input_ids, positions, intermediate_tensors, inputs_embeds)

@@ -8,6 +8,7 @@ signature (model.py:54-86).
 """
 from __future__ import annotations
 
+import collections
 import ctypes
 import threading
 import time
@@ -260,7 +261,12 @@ class MkModel:
             pass
 
 
-_MODELS: dict = {}
+# runtime.forward's packed models: key (storage, shapes, quant, shape arguments) -> (version counters of
+# the tensors, MkModel), least recently used first.  The packed copy is rebuilt when a caller updated
+# any of the tensors in place (torch bumps a tensor's version counter on every in-place write), as the
+# reference op reads the tensors it is passed on every call.
+_MODELS: "collections.OrderedDict" = collections.OrderedDict()
+MAX_CACHED_MODELS = 2
 
 
 def _validate_attn(attn: str) -> None:
@@ -280,15 +286,22 @@ def forward(input_ids, embed, cos, sin, final_norm, w_qkv, w_o, w_gu, w_down, s_
                a_qkv, a_o, a_gu, a_down, wl_qkv, wl_o, wl_gu, wl_down)
     key = (tuple(t.data_ptr() for t in tensors), tuple(tuple(t.shape) for t in tensors), quant, n_q, n_kv,
            head_dim, float(eps))
-    m = _MODELS.get(key)
-    if m is None:
+    versions = tuple(t._version for t in tensors)
+    hit = _MODELS.get(key)
+    if hit is not None and hit[0] != versions:        # updated in place since it was packed: re-pack
+        _MODELS.pop(key)[1].close()
+        hit = None
+    if hit is None:
+        while len(_MODELS) >= MAX_CACHED_MODELS:
+            _MODELS.popitem(last=False)[1][1].close()
         w = dict(zip(WEIGHT_ORDER, (w_qkv, w_o, w_gu, w_down, s_qkv, s_o, s_gu, s_down,
                                     a_qkv, a_o, a_gu, a_down, wl_qkv, wl_o, wl_gu, wl_down)))
-        m = _MODELS[key] = MkModel(w, embed, cos, sin, final_norm, quant, n_q, n_kv, head_dim, eps)
-    return m.forward(input_ids, bs, seq)
+        hit = _MODELS[key] = (versions, MkModel(w, embed, cos, sin, final_norm, quant, n_q, n_kv, head_dim, eps))
+    _MODELS.move_to_end(key)
+    return hit[1].forward(input_ids, bs, seq)
 
 
 def clear_cache() -> None:
-    for m in _MODELS.values():
+    for _, m in _MODELS.values():
         m.close()
     _MODELS.clear()

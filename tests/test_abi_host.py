@@ -194,3 +194,21 @@ def test_gemm_rejects_operands_of_4_gib():
     # B: 40000 rows x 65536 bf16
     rc = lib.mk_gemm(0, 4, p, 65536, p, 65536, 256, 40000, 65536, p, 40000, None, 0, None, None, None, None)
     assert rc == -1 and b"4 GiB" in lib.mk_last_error()
+
+
+def test_gemm_k_alignment_by_path():
+    """K bytes: a multiple of 64 on the tiled kernels (M > 32), of 32 on the weight-streaming kernel
+    (M <= 32); a 32-byte K at M > 32 is MK_EINVAL before any launch (include/mk.h, mk_gemm)."""
+    from minicpm5_mk import _lib
+
+    lib = _lib.load()
+    p = ctypes.c_void_p(0x10000)
+    # int8, K = 32 bytes, M = 64: tiled path -> rejected
+    rc = lib.mk_gemm(1, 3, p, 32, p, 32, 64, 64, 32, p, 64, None, 0, None, None, None, None)
+    assert rc == -1 and b"multiple of 64" in lib.mk_last_error()
+    # bf16, K = 16 elements = 32 bytes, M = 64: rejected the same way
+    rc = lib.mk_gemm(0, 4, p, 16, p, 16, 64, 64, 16, p, 64, None, 0, None, None, None, None)
+    assert rc == -1 and b"multiple of 64" in lib.mk_last_error()
+    # K = 16 bytes is below either path's granule
+    rc = lib.mk_gemm(1, 3, p, 16, p, 16, 8, 64, 16, p, 64, None, 0, None, None, None, None)
+    assert rc == -1 and b"multiple of 32" in lib.mk_last_error()

@@ -133,6 +133,14 @@ def fake_vllm(monkeypatch):
         def __init__(self, *, vllm_config, prefix=""):
             super().__init__()
             self.stock_calls = 0
+            hf = vllm_config.model_config.hf_config
+            self.model = torch.nn.Module()
+            self.model.embed_tokens = torch.nn.Embedding(8, hf.hidden_size).to(torch.bfloat16)
+            self.model.layers = torch.nn.ModuleList([torch.nn.Linear(4, 4) for _ in range(hf.num_hidden_layers)])
+            self.lm_head = torch.nn.Linear(4, 4)
+
+        def load_weights(self, weights):
+            return {name for name, _ in weights}
 
         def forward(self, input_ids, positions, intermediate_tensors=None, inputs_embeds=None):
             self.stock_calls += 1
@@ -194,3 +202,216 @@ def test_model_class_dispatch(fake_vllm):
     STATE.set((4, 128), "ok")                                                # more tokens than the step holds
     assert m(ids, pos) == "stock"
     assert m._mk_counts["mk"] == 1 and m._mk_counts["mk:2x128"] == 1
+
+
+HF_TINY = dict(hidden_size=256, num_attention_heads=16, num_key_value_heads=2, head_dim=64, num_hidden_layers=3,
+               intermediate_size=768, vocab_size=32768, rms_norm_eps=1e-6, rope_theta=1e4)
+
+
+def _vllm_cfg(max_len=8256, prefix_caching=False):
+    return SimpleNamespace(model_config=SimpleNamespace(hf_config=SimpleNamespace(**HF_TINY), max_model_len=max_len),
+                           parallel_config=SimpleNamespace(pipeline_parallel_size=1, tensor_parallel_size=1),
+                           cache_config=SimpleNamespace(enable_prefix_caching=prefix_caching))
+
+
+class _FakeMkModel:
+    """Stands in for runtime.MkModel (libmk needs a GPU): records the calls, returns (max(8, B), H) rows."""
+    quant = "int8d"
+
+    def __init__(self, *args, **kwargs):
+        self.calls = []
+
+    def forward(self, ids, bs, seq):
+        self.calls.append((bs, seq))
+        return torch.ones(max(8, bs), HF_TINY["hidden_size"], dtype=torch.bfloat16)
+
+    def precompile(self, shapes, logits=False, log=None):
+        pass
+
+
+def _load(m, model_mod, monkeypatch):
+    """load_weights with the weight preparation and the device model replaced by doubles."""
+    from minicpm5_mk.runtime import WEIGHT_ORDER
+    monkeypatch.setattr(model_mod, "MkModel", _FakeMkModel)
+    monkeypatch.setattr(model_mod, "prepare_mk_weights",
+                        lambda *a, **k: {**{n: torch.zeros(1) for n in WEIGHT_ORDER}, "cos": torch.zeros(1),
+                                         "sin": torch.zeros(1)})
+    H = HF_TINY["hidden_size"]
+    names = [("model.embed_tokens.weight", torch.zeros(8, H)), ("model.norm.weight", torch.ones(H)),
+             ("model.layers.0.mlp.down_proj.weight", torch.zeros(H, 4))]
+    return m.load_weights(iter(names))
+
+
+def test_stock_freed_mode_and_status(fake_vllm, monkeypatch, tmp_path):
+    """MINICPM5_MK_FREE_STOCK=1 (plugin/minicpm5_mk/model.py:700-705, :787-794): the stock decoder
+    weights are dropped after the build, a dummy run returns zeros, any other ineligible step raises;
+    the status file carries the reference's keys (:683-689) and the stock reasons (:777-785)."""
+    import json
+    model_mod, _ = fake_vllm
+    monkeypatch.setenv("MINICPM5_MK_FREE_STOCK", "1")
+    monkeypatch.setenv("MINICPM5_MK_STATUS_DIR", str(tmp_path))
+    m = model_mod.MiniCPM5MegakernelForCausalLM(vllm_config=_vllm_cfg())
+    assert m._mk_enabled
+    assert _load(m, model_mod, monkeypatch) >= {"model.norm.weight"}
+    assert m._mk_stock_freed and all(p.numel() == 0 for p in m.model.layers.parameters())
+    st = json.loads((tmp_path / "minicpm5_mk_status_rank0.json").read_text())
+    assert st["stock_freed"] is True and st["tp"] == 1 and st["rank"] == 0 and st["multicore_modes"] == []
+    assert st["quant"] == st["quant_tp"] and st["shapes"] == {} and "stock_reasons" not in st
+    ids, pos = torch.arange(2 * 128), torch.arange(128).repeat(2)
+    STATE.set((2, 128), "ok")
+    out = m(ids, pos)
+    assert out.shape == (256, HF_TINY["hidden_size"]) and m._mk_model.calls == [(2, 128)]
+    STATE.set(None, "dummy")
+    z = m(ids, pos)
+    assert z.dtype == torch.bfloat16 and z.shape == (256, HF_TINY["hidden_size"]) and not z.any()
+    STATE.set(None, "continuation")
+    with pytest.raises(RuntimeError, match="stock weights were freed"):
+        m(ids, pos)
+    st = json.loads((tmp_path / "minicpm5_mk_status_rank0.json").read_text())
+    assert st["shapes"] == {"mk:2x128": {"mode": "single", "quant": "int8d"}}
+    assert st["stock_reasons"] == ["continuation"]                       # dummy runs are not recorded
+    assert m._mk_counts["stock:dummy"] == 1 and m._mk_counts["stock:continuation"] == 1
+
+
+def test_stock_path_kept_without_free_stock(fake_vllm, monkeypatch, tmp_path, caplog):
+    import json
+    import logging
+    model_mod, _ = fake_vllm
+    monkeypatch.delenv("MINICPM5_MK_FREE_STOCK", raising=False)
+    monkeypatch.setenv("MINICPM5_MK_STATUS_DIR", str(tmp_path))
+    monkeypatch.setenv("MINICPM5_MK_LOG_EVERY", "2")
+    m = model_mod.MiniCPM5MegakernelForCausalLM(vllm_config=_vllm_cfg())
+    _load(m, model_mod, monkeypatch)
+    assert not m._mk_stock_freed and all(p.numel() > 0 for p in m.model.layers.parameters())
+    ids, pos = torch.arange(256), torch.arange(128).repeat(2)
+    with caplog.at_level(logging.INFO, logger="vllm.minicpm5_mk"):
+        for reason in ("max_tokens", "max_tokens", "ragged"):
+            STATE.set(None, reason)
+            assert m(ids, pos) == "stock"
+    st = json.loads((tmp_path / "minicpm5_mk_status_rank0.json").read_text())
+    assert st["stock_freed"] is False and st["stock_reasons"] == ["max_tokens", "ragged"]
+    assert m._mk_counts["stock"] == 3 and m._mk_counts["stock:max_tokens"] == 2
+    assert sum("counts=" in r.getMessage() for r in caplog.records) == 1    # every 2nd forward
+
+
+def test_prefix_caching_turns_fast_path_off(fake_vllm, monkeypatch):
+    """A fast-path prefill writes no KV cache, so with prefix caching a later request sharing its
+    prefix would read unwritten blocks on the stock path: the fast path is off, and megakernel-only
+    mode refuses to start."""
+    model_mod, _ = fake_vllm
+    monkeypatch.delenv("MINICPM5_MK_FREE_STOCK", raising=False)
+    m = model_mod.MiniCPM5MegakernelForCausalLM(vllm_config=_vllm_cfg(prefix_caching=True))
+    assert not m._mk_enabled
+    monkeypatch.setenv("MINICPM5_MK_FREE_STOCK", "1")
+    with pytest.raises(RuntimeError, match="prefix caching"):
+        model_mod.MiniCPM5MegakernelForCausalLM(vllm_config=_vllm_cfg(prefix_caching=True))
+
+
+def test_runner_hook_follows_latest_model(fake_vllm):
+    """A model built after an earlier one was freed re-points the runner hook at itself."""
+    import gc
+    model_mod, Runner = fake_vllm
+    a = model_mod.MiniCPM5MegakernelForCausalLM(vllm_config=_vllm_cfg(max_len=8256))
+    del a
+    gc.collect()
+    b = model_mod.MiniCPM5MegakernelForCausalLM(vllm_config=_vllm_cfg(max_len=16384))
+    runner, so = _fake_runner(["a"], [0], [16384], [16384], [SP1])
+    r = Runner()
+    r.__dict__.update(runner.__dict__)
+    r._prepare_inputs(so)
+    assert STATE.take() == ((1, 16384), "ok")
+    assert b._mk_max_seq == 16384
+
+
+class _FakeEngineCore:
+    def __init__(self, vllm_config):
+        self.vllm_config = vllm_config
+
+
+class _FakeKVManager:
+    empty_kv_cache_blocks = "EMPTY"
+
+    def allocate_slots(self, request, num_new_tokens, *args, **kwargs):
+        return "BLOCKS"
+
+
+def _req(seq=8192, computed=0, sp=SP1):
+    return SimpleNamespace(num_prompt_tokens=seq, num_computed_tokens=computed, sampling_params=sp)
+
+
+def test_kv_alloc_skip(monkeypatch):
+    """KV-allocation skip (plugin/minicpm5_mk/__init__.py:154-206): only in megakernel-only mode, only for
+    an engine serving the architecture without prefix caching, only for full fresh max_tokens=1 prefills
+    with fast-path sampling and a served length; every other request gets vLLM's allocation."""
+    import minicpm5_mk as pkg
+    monkeypatch.setattr(pkg, "ENGINE_SERVES_ARCH", {"active": False, "prefix_caching": False, "max_model_len": 0})
+
+    class Core(_FakeEngineCore):
+        pass
+
+    class KV(_FakeKVManager):
+        pass
+
+    pkg.install_kv_skip(Core, KV)
+    pkg.install_kv_skip(Core, KV)                                           # idempotent
+    mc = SimpleNamespace(architectures=[pkg.ARCH], hf_config=SimpleNamespace(architectures=[]), max_model_len=8256)
+    cfg = SimpleNamespace(model_config=mc, cache_config=SimpleNamespace(enable_prefix_caching=False))
+    Core(cfg)
+    kv = KV()
+    monkeypatch.delenv("MINICPM5_MK_FREE_STOCK", raising=False)
+    assert kv.allocate_slots(_req(), 8192) == "BLOCKS"                      # stock path may run: allocate
+    monkeypatch.setenv("MINICPM5_MK_FREE_STOCK", "1")
+    assert kv.allocate_slots(_req(), 8192) == "EMPTY"
+    assert kv.allocate_slots(_req(1024), 1024) == "EMPTY"
+    assert kv.allocate_slots(_req(384), 384) == "EMPTY"
+    assert kv.allocate_slots(_req(), 2048) == "BLOCKS"                      # chunked prefill
+    assert kv.allocate_slots(_req(computed=8192), 1) == "BLOCKS"           # continuation / decode
+    assert kv.allocate_slots(_req(sp=SamplingParams(max_tokens=4)), 8192) == "BLOCKS"
+    assert kv.allocate_slots(_req(sp=None), 8192) == "BLOCKS"
+    assert kv.allocate_slots(_req(sp=SamplingParams(max_tokens=1, repetition_penalty=1.2)), 8192) == "BLOCKS"
+    assert kv.allocate_slots(_req(1000), 1000) == "BLOCKS"                 # length not served
+    assert kv.allocate_slots(_req(1152), 1152) == "BLOCKS"
+    assert kv.allocate_slots(_req(16384), 16384) == "BLOCKS"               # beyond the engine's max length
+    monkeypatch.setenv("MINICPM5_MK_ENABLE", "0")
+    assert kv.allocate_slots(_req(), 8192) == "BLOCKS"
+    monkeypatch.delenv("MINICPM5_MK_ENABLE")
+    Core(SimpleNamespace(model_config=mc, cache_config=SimpleNamespace(enable_prefix_caching=True)))
+    assert kv.allocate_slots(_req(), 8192) == "BLOCKS"                      # prefix caching: never skip
+    other = SimpleNamespace(architectures=["LlamaForCausalLM"], hf_config=SimpleNamespace(architectures=[]),
+                            max_model_len=8256)
+    Core(SimpleNamespace(model_config=other, cache_config=SimpleNamespace(enable_prefix_caching=False)))
+    assert kv.allocate_slots(_req(), 8192) == "BLOCKS"                      # another model's engine
+    Core(SimpleNamespace(model_config=SimpleNamespace(architectures=None,
+                                                      hf_config=SimpleNamespace(architectures=[pkg.ARCH]),
+                                                      max_model_len=8256), cache_config=None))
+    assert kv.allocate_slots(_req(), 8192) == "EMPTY"                       # architecture from the HF config
+
+
+def test_single_step_batch_queue():
+    """Scoring batches run as one step when the batch queue is deeper than one
+    (plugin/minicpm5_mk/__init__.py:208-245)."""
+    import minicpm5_mk as pkg
+
+    class Core:
+        def __init__(self, waiting, running=(), bq=(), bq_size=2):
+            self.batch_queue = list(bq)
+            self.batch_queue_size = bq_size
+            self.scheduler = SimpleNamespace(waiting=list(waiting), running=list(running), max_num_running_reqs=4,
+                                             max_num_scheduled_tokens=32768)
+            self.seen = []
+
+        def step_with_batch_queue(self):
+            self.seen.append(self.batch_queue_size)
+            return "stepped"
+
+    pkg.install_single_step(Core)
+    pkg.install_single_step(Core)
+    four = [_req() for _ in range(4)]
+    c = Core(four)
+    assert c.step_with_batch_queue() == "stepped" and c.seen == [1] and c.batch_queue_size == 2
+    for core in (Core(four + [_req()]),                                      # more than max running
+                 Core([_req(), _req(sp=SamplingParams(max_tokens=2))]),     # not all scoring
+                 Core([_req(16384), _req(16384), _req(16384)]),             # over the token budget
+                 Core(four, running=[1]), Core(four, bq=[1]), Core(four, bq_size=1), Core([])):
+        core.step_with_batch_queue()
+        assert core.seen == [core.batch_queue_size]

@@ -603,6 +603,48 @@ def test_runtime_forward_reference_signature(quant):
 
 
 @pytest.mark.gpu
+def test_runtime_forward_repacks_after_in_place_update():
+    """runtime.forward re-packs a weight set that the caller updated in place (same storage, new
+    values): the reference op reads its weight arguments on every call (model.py:749-751), so the next
+    call must return what a model built from the updated tensors returns.  The cache holds at most
+    MAX_CACHED_MODELS weight sets."""
+    from minicpm5_mk import runtime
+    from minicpm5_mk.config import preset
+    from minicpm5_mk.mk_weights import prepare_mk_weights
+    from minicpm5_mk.runtime import WEIGHT_ORDER, MkModel
+    from minicpm5_mk.synth import random_hf_state_dict, random_token_ids
+
+    dev = _dev()
+    cfg = preset("tiny")
+    quant = "int8d:qkv+gu|sq|lastbf16|fqkv|fmlp"
+    sd = random_hf_state_dict(cfg)
+    w = prepare_mk_weights(sd, cfg.as_mk_cfg(), quant, 1024, log=lambda *a: None)
+    wd = [w[k].to(dev) for k in WEIGHT_ORDER]
+    embed, fnorm = sd["model.embed_tokens.weight"].to(dev), sd["model.norm.weight"].to(dev)
+    cos, sin = w["cos"].to(dev), w["sin"].to(dev)
+    bs, seq = 2, 256
+    ids = random_token_ids(bs, seq, seed=3).reshape(-1).to(dev)
+    args = (bs, seq, quant, cfg.n_q, cfg.n_kv, cfg.head_dim, cfg.eps, "auto")
+    runtime.clear_cache()
+    out0 = runtime.forward(ids, embed, cos, sin, fnorm, *wd, *args)
+    w_o = wd[WEIGHT_ORDER.index("w_o")]
+    assert w_o.dtype == BF16
+    w_o.mul_(0.5)                                            # in place: same storage, new values
+    out1 = runtime.forward(ids, embed, cos, sin, fnorm, *wd, *args)
+    assert not torch.equal(out0, out1)
+    m = MkModel(dict(zip(WEIGHT_ORDER, wd)), embed, cos, sin, fnorm, quant, cfg.n_q, cfg.n_kv, cfg.head_dim, cfg.eps)
+    ref = m.forward(ids, bs, seq)
+    m.close()
+    assert torch.equal(out1, ref)
+    assert len(runtime._MODELS) == 1                        # the stale packing was replaced, not kept
+    assert torch.equal(runtime.forward(ids, embed, cos, sin, fnorm, *wd, *args), out1)   # no update: reused
+    for i in range(3):                                       # other weight sets: bounded cache
+        runtime.forward(ids, embed, cos, sin, fnorm, *[t.clone() for t in wd], *args)
+    assert len(runtime._MODELS) == runtime.MAX_CACHED_MODELS
+    runtime.clear_cache()
+
+
+@pytest.mark.gpu
 def test_precompile_captures_without_running():
     """MkModel.precompile (MINICPM5_MK_PRECOMPILE, model.py:690-698) captures one hipGraph per shape
     without running it: the output buffers keep their contents, the graph count grows by one per new
