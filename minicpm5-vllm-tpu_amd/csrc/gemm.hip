@@ -948,6 +948,29 @@ int choose_cfg(const GemmArgs& g) {
   return best;
 }
 
+// Tile-order group height (rows of tiles per group; the kernel walks each group column by column and
+// gives every XCD a contiguous range of work).  Problems of more than one round of tiles: the
+// workgroups an XCD runs at once (its CUs times the workgroups per CU) span min(16, column tiles)
+// columns.  Measured in the whole model on MI355X (bitwise-identical outputs), against the former fixed
+// height of 8 this takes the routed QKV projection from 57.6 to 52.8 us at 1B (1, 8192) and from 70.3
+// to 63.3 us at 2B -- with whole rows of tiles per XCD the K RoPE / V^T routing tiles, the slow ones,
+// no longer all land on the same XCDs -- the 1B gate/up from 134.5 to 132 us (522 to 504 us at
+// (4, 8192)) and the 2B gate/up from 218.9 to 216.9 us; O and down move by under 2 %.  One-round
+// problems (short prompts, whose weights arrive cold from HBM) keep 8: spreading an XCD's tiles over
+// 16 columns there makes every XCD stream all of the weight matrix (2B down projection at M = 1024:
+// 42 -> 57 us).
+int group_height(int tiles_n, int tiles_m, int occ) {
+  static const int cus = [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      n = 0;
+    return n > 0 ? n : 256;
+  }();
+  const int per_xcd = std::max(1, cus / 8) * occ;
+  if ((long)tiles_n * tiles_m <= 8L * per_xcd) return std::min(8, tiles_m);
+  return std::max(1, std::min(tiles_m, per_xcd / std::min(16, std::max(1, tiles_n))));
+}
+
 template <class C, GemmIn IN, Epi EPI>
 void launch_c(const GemmArgs& g0, hipStream_t st) {
   dim3 grid((g0.N + C::BN - 1) / C::BN, (g0.M + C::BM - 1) / C::BM);
@@ -957,7 +980,7 @@ void launch_c(const GemmArgs& g0, hipStream_t st) {
       const char* e = std::getenv("MK_GEMM_GM");   // tuning override
       return e ? std::atoi(e) : 0;
     }();
-    g.gm = forced > 0 ? forced : 8;
+    g.gm = forced > 0 ? forced : group_height((int)grid.x, (int)grid.y, C::OCC);
   }
   g.gm = std::min<int>(g.gm, grid.y);
   hipLaunchKernelGGL((gemm_kernel<C::BM, C::BN, C::WGM, C::WGN, C::NST, C::OCC, C::LOOP, IN, EPI>), grid, dim3(C::NTH),

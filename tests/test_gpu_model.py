@@ -427,8 +427,11 @@ def test_short_prompt_batch_invariance(name):
 
 
 def test_full_model_bf16_1b_hd96_argmax():
-    """The 1B-hd96 golden forward's model with every linear in bf16 (quant "bf16"), to separate
-    the W8A8 numerics from the kernels in the top-1 decision (golden top-1 / top-2 margin 0.029)."""
+    """BASELINE config 1 (the FP32 golden forward of MiniCPM5-1B-hd96 at (1, 8192)) on the GPU with every
+    linear in bf16 (quant "bf16"): the argmax is the golden's top-1, exactly.  The GPU output is
+    deterministic (fixed summation orders), so this is a stable check; it separates the kernels from the
+    W8A8 numerics, whose quantisation error (mean |dlogit| 0.048) exceeds this golden's top-1 / top-2
+    margin (0.029), so the W8A8 test of this model is tie-aware."""
     from minicpm5_mk.synth import random_token_ids
 
     gold, meta = _golden("1b-hd96")
@@ -443,8 +446,7 @@ def test_full_model_bf16_1b_hd96_argmax():
     print(f"[bf16] 1b-hd96: vs golden max {err.max():.4f} mean {err.mean():.4f}; vs emulator max {eerr.max():.4f}; "
           f"argmax GPU {int(lg.argmax())} emulator {int(e.argmax())} golden {int(g.argmax())}", flush=True)
     assert err.max() <= 0.25 and eerr.max() <= 0.1
-    lpg = torch.log_softmax(g, -1)
-    assert float(lpg.max() - lpg[int(lg.argmax())]) <= 0.1
+    assert int(lg.argmax()) == int(g.argmax())
     m.release_buffers()
 
 
