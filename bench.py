@@ -44,8 +44,8 @@ PEAK = {"bf16": 2516.6, "int8": 5033.2, "fp8": 5033.2, "hbm": 8000.0}   # MI355X
 METRIC = "prefill tokens/sec at (B,8192) B=1..32, 1B and 2B arch; p50 ms at (1,8192)"
 # HBM bytes per attn_fwd_kernel launch measured by rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (scaled by a
 # 256 MiB copy's counters) for the default workload; (arch, B, S, quant) -> (bytes, source file)
-ATTN_TRAFFIC = {("1b", 1, 8192, "auto"): (77.0e6 + 33.6e6, "profiles/mfma_util_hbm_1b_b1_s8192.txt"),
-                ("2b", 1, 8192, "auto"): (77.1e6 + 33.6e6, "profiles/mfma_util_hbm_2b_b1_s8192.txt")}
+ATTN_TRAFFIC = {("1b", 1, 8192, "auto"): (77.1e6 + 33.6e6, "profiles/mfma_util_hbm_1b_b1_s8192.txt"),
+                ("2b", 1, 8192, "auto"): (77.2e6 + 33.6e6, "profiles/mfma_util_hbm_2b_b1_s8192.txt")}
 DEFAULT_SWEEP = "1b:4,8,16,32;2b:1,4,8,16,32;1b-hd96:1,4,8,16,32"
 
 
@@ -268,9 +268,9 @@ def cpu_baseline(cfg, runs, seq=8192, batch=1):
         per_batch.append({"batch": b, "tokens_per_s": round(tps, 1), "p50_ms": round(med * 1e3 * b / batch, 1),
                           "timed": b == batch,
                           **({} if b == batch else {"extrapolated_from_batch": batch})})
-    what = "one whole" if batch == 1 else f"{batch} whole"
+    what = f"one whole {seq}-token sequence" if batch == 1 else f"{batch} whole {seq}-token sequences"
     return {"value": round(tps, 1), "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"oracle FP32 forward (oracle/golden.py) of {what} {seq}-token sequence(s) of {cfg.name} "
+            "sample": f"oracle FP32 forward (oracle/golden.py) of {what} of {cfg.name} "
                       f"({cfg.num_layers} layers + final norm + LM head each), {runs} timed runs after a one-layer "
                       f"warm-up: {', '.join(f'{t:.1f}' for t in times)} s (median {med:.1f} s); weights "
                       f"generated and upcast in {t_load:.1f} s (untimed)",
