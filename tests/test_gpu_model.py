@@ -381,8 +381,8 @@ TWO_LAYER = {"1b": (0.07, 0.012), "1b-hd96": (0.08, 0.012), "2b": (0.15, 0.023)}
 
 # (preset, batch sizes): the 1B-hd96 and 2B prefill workloads at B = 4..32, plus the reference's 1B; 2B at
 # B = 48 runs in two chunks (42 + 6 sequences: the (T, I) bf16 activation of 48 x 8192 tokens exceeds 4 GiB).
-BATCH = [("1b-hd96", 4), ("1b-hd96", 8), ("1b-hd96", 16), ("1b-hd96", 32), ("1b", 4), ("1b", 32), ("2b", 4), ("2b", 32),
-         ("2b", 48)]
+BATCH = [("1b-hd96", 4), ("1b-hd96", 8), ("1b-hd96", 16), ("1b-hd96", 32), ("1b", 4), ("1b", 32), ("2b", 4), ("2b", 8),
+         ("2b", 16), ("2b", 32), ("2b", 48)]
 
 
 @pytest.mark.parametrize("name,B", BATCH)
@@ -404,6 +404,42 @@ def test_full_batch_invariance_s8192(name, B):
         assert torch.equal(h1[0], hB[b]) and torch.equal(l1[0], lB[b]), f"row {b} differs from its single run"
     _golden_checks(name, lB[0].cpu(), torch.from_numpy(gold["logits"][0]), *tol)
     m.release_buffers()
+
+
+@pytest.mark.parametrize("name,B,S", [("tiny", 1, 896), ("tiny", 3, 384), ("tiny", 2, 2048), ("tiny-hd96", 2, 1152)])
+def test_last_layer_step_isolated(name, B, S):
+    """The last-token layer (mk_jax.py:492-520: K/V projection over all S tokens, q / O / gate-up / down on
+    the last token only, chunked single-query attention and its merge, bf16 weights) on its own.  Layer
+    0's O and down projections are zero, so the residual stream it passes on is the embedding exactly
+    (bf16(x + 0) = x); the GPU's final-normed rows and logits are then compared with
+    final_norm(emulate.last_layer_step(embedding)).  Bounds: the two sides differ only in f32 summation
+    orders, so a hidden value may differ by a bf16 rounding or two (measured: max 1 ulp, 0.0156 at
+    |values| ~3.3; mean 5e-4 .. 2.3e-3; logits max 3e-3 .. 8e-3)."""
+    from minicpm5_mk.config import preset
+    from minicpm5_mk.synth import random_hf_state_dict, random_token_ids
+    from oracle import emulate
+
+    dev = _dev()
+    cfg = preset(name).replace(num_layers=2)
+    sd = random_hf_state_dict(cfg, seed=7)
+    sd["model.layers.0.self_attn.o_proj.weight"].zero_()
+    sd["model.layers.0.mlp.down_proj.weight"].zero_()
+    quant = "int8d:qkv+gu|sq|lastbf16|fqkv|fmlp"
+    m, w = _build(cfg, quant, sd, S + 64, dev)
+    ids = random_token_ids(B, S, seed=S + B)
+    print(f"[last layer] {name} B={B} S={S}", flush=True)
+    h, lg = m.forward(ids.reshape(-1).to(dev), B, S, logits=True)
+    h, lg = h[:B].float().cpu(), lg.float().cpu()
+    x = sd["model.embed_tokens.weight"][ids.long()].to(BF16)
+    x_last = emulate.last_layer_step(x, w, w["cos"], w["sin"], cfg.n_q, cfg.n_kv, cfg.head_dim, cfg.eps)
+    ref = (emulate._rms_unit_bf16(x_last, cfg.eps) * sd["model.norm.weight"].float()).to(BF16).float()
+    lref = ref @ sd["lm_head.weight"].float().t()
+    eh, el = (h - ref).abs(), (lg - lref).abs()
+    print(f"[last layer] hidden max {eh.max():.4g} mean {eh.mean():.3g} (|ref| max {ref.abs().max():.3g}); "
+          f"logits max {el.max():.4g}; argmax {lg.argmax(-1).tolist()} vs {lref.argmax(-1).tolist()}", flush=True)
+    assert eh.max() <= 0.012 * ref.abs().max() and eh.mean() <= 1.5e-3 * ref.abs().max()
+    assert el.max() <= 0.02 and torch.equal(lg.argmax(-1), lref.argmax(-1))
+    m.close()
 
 
 @pytest.mark.parametrize("name", ["1b", "2b"])
