@@ -91,29 +91,33 @@ class MiniCPM5MegakernelForCausalLM(LlamaForCausalLM):
         self._mk_model = None
         self._mk_status = None
         self._mk_stock_freed = False
+        off = []   # why the fast path is off
+
+        def disable(reason: str) -> None:
+            logger.warning("minicpm5_mk: %s; fast path disabled", reason)
+            off.append(reason)
+            self._mk_enabled = False
+
         cache_cfg = getattr(vllm_config, "cache_config", None)
         if self._mk_enabled and getattr(cache_cfg, "enable_prefix_caching", False):
-            if _free_stock():
-                raise RuntimeError("minicpm5_mk: MINICPM5_MK_FREE_STOCK=1 needs the fast path, which does not run with "
-                                   "prefix caching (its prefills write no KV cache); start the engine with "
-                                   "enable_prefix_caching=False")
-            logger.warning("minicpm5_mk: prefix caching is on; fast path disabled (its prefills write no KV cache)")
-            self._mk_enabled = False
+            disable("prefix caching is on (a fast-path prefill writes no KV cache; start the engine with "
+                    "enable_prefix_caching=False)")
         rope = getattr(hf, "rope_scaling", None) or getattr(hf, "rope_parameters", None)
         if isinstance(rope, dict) and rope.get("rope_type", rope.get("type", "default")) not in (None, "default"):
-            logger.warning("minicpm5_mk: rope_scaling=%s unsupported; fast path disabled", rope)
-            self._mk_enabled = False
+            disable(f"rope_scaling={rope} unsupported")
         if vllm_config.parallel_config.pipeline_parallel_size != 1 or vllm_config.parallel_config.tensor_parallel_size != 1:
-            logger.warning("minicpm5_mk: one GPU per model only (no PP / TP); fast path disabled")
-            self._mk_enabled = False
+            disable("one GPU per model only (no PP / TP)")
         try:
             self._mk_cfg.validate()
         except ValueError as e:
-            logger.warning("minicpm5_mk: %s; fast path disabled", e)
-            self._mk_enabled = False
+            disable(str(e))
         if self._mk_enabled and not _hook_vllm_runner(self):
-            logger.warning("minicpm5_mk: vLLM GPU model runner not found; fast path disabled")
-            self._mk_enabled = False
+            disable("vLLM GPU model runner not found")
+        # Megakernel-only mode lets the engine skip KV allocation for fast-path requests, which is only
+        # correct while this model serves them on the fast path: with the fast path off for any reason
+        # other than MINICPM5_MK_ENABLE=0 (which turns the KV skip off too), refuse to start.
+        if off and _free_stock() and os.environ.get("MINICPM5_MK_ENABLE", "1") != "0":
+            raise RuntimeError("minicpm5_mk: MINICPM5_MK_FREE_STOCK=1 needs the fast path, which is off: " + "; ".join(off))
 
     def load_weights(self, weights: Iterable[tuple[str, torch.Tensor]]) -> set[str]:
         if not self._mk_enabled:

@@ -307,6 +307,29 @@ def test_prefix_caching_turns_fast_path_off(fake_vllm, monkeypatch):
         model_mod.MiniCPM5MegakernelForCausalLM(vllm_config=_vllm_cfg(prefix_caching=True))
 
 
+def test_free_stock_refuses_a_disabled_fast_path(fake_vllm, monkeypatch):
+    """Megakernel-only mode lets the engine skip KV allocation, so a model whose fast path is off for
+    any reason (here: tensor parallelism, unsupported rope scaling) must not start in that mode; with
+    MINICPM5_MK_ENABLE=0 the KV skip is off as well and the stock model starts normally."""
+    model_mod, _ = fake_vllm
+    monkeypatch.setenv("MINICPM5_MK_FREE_STOCK", "1")
+    cfg = _vllm_cfg()
+    cfg.parallel_config.tensor_parallel_size = 2
+    with pytest.raises(RuntimeError, match="PP / TP"):
+        model_mod.MiniCPM5MegakernelForCausalLM(vllm_config=cfg)
+    cfg = _vllm_cfg()
+    cfg.model_config.hf_config.rope_scaling = {"rope_type": "yarn", "factor": 4.0}
+    with pytest.raises(RuntimeError, match="rope_scaling"):
+        model_mod.MiniCPM5MegakernelForCausalLM(vllm_config=cfg)
+    monkeypatch.setenv("MINICPM5_MK_ENABLE", "0")
+    m = model_mod.MiniCPM5MegakernelForCausalLM(vllm_config=cfg)
+    assert not m._mk_enabled
+    monkeypatch.delenv("MINICPM5_MK_FREE_STOCK")
+    monkeypatch.delenv("MINICPM5_MK_ENABLE")
+    m = model_mod.MiniCPM5MegakernelForCausalLM(vllm_config=cfg)   # stock-capable: warns, keeps stock
+    assert not m._mk_enabled
+
+
 def test_runner_hook_follows_latest_model(fake_vllm):
     """A model built after an earlier one was freed re-points the runner hook at itself."""
     import gc
