@@ -339,6 +339,45 @@ def test_full_model_vs_emulator(name, tol_max, tol_mean):
     assert err.max() <= tol_max and err.mean() <= tol_mean
 
 
+# The quantisation variants (fp8 dynamic on the CDNA4 fp8 MFMA, static int8) at full size: MiniCPM5-1B at
+# (1, 8192), GPU vs the CPU emulation of the same numerics (tests/golden/emulate_1b_<tag>_b1_s8192.npz, written
+# by make_emulator_fixture.py --quant ...) and vs the FP32 golden.  (quant, fixture tag, max, mean): bounds
+# 1.5x the measured GPU-vs-emulator error, as for the W8A8 fixtures above.  The emulations themselves err
+# vs FP32: fp8d max 0.628 / mean 0.117, mean |dlogprob| top-20 0.129, argmax the golden's #3 (token 6581,
+# 0.166 nats below the top-1: e4m3's 3-bit mantissa moves it); static int8 0.211 / 0.038, 0.050, top-1.
+# Argmax rule: the golden top-1 or the token the emulation of the same numerics picks.
+# Measured on MI355X: fp8d 0.329 / 0.058 (argmax = the emulation's), static int8 0.161 / 0.027.
+QVARIANTS = [("fp8d:qkv+gu|sq|lastbf16", "fp8d", 0.5, 0.087), ("int8:qkv+gu|sq|lastbf16", "int8", 0.25, 0.041)]
+
+
+@pytest.mark.parametrize("quant,tag,tol_max,tol_mean", QVARIANTS)
+def test_full_model_quant_variants(quant, tag, tol_max, tol_mean):
+    from minicpm5_mk.synth import random_token_ids
+
+    fx = np.load(os.path.join(HERE, "golden", f"emulate_1b_{tag}_b1_s8192.npz"))
+    emeta = json.loads(bytes(fx["meta"]).decode())
+    gold, meta = _golden("1b")
+    m = _full_model("1b", quant)
+    assert emeta["quant"] == m.quant == quant
+    ids = random_token_ids(1, 8192, seed=emeta["id_seed"])
+    _, lg = m.forward(ids.reshape(-1).to(_dev()), 1, 8192, logits=True)
+    lg = lg.cpu()[0]
+    e = torch.from_numpy(fx["logits"][0])
+    g = torch.from_numpy(gold["logits"][0])
+    err, gerr = (lg - e).abs(), (lg - g).abs()
+    lp, lpg = torch.log_softmax(lg, -1), torch.log_softmax(g, -1)
+    top = torch.topk(lpg, 20).indices
+    dlp = float((lp[top] - lpg[top]).abs().mean())
+    print(f"[variant] {quant}: GPU vs emulator max {err.max():.4f} mean {err.mean():.4f}; vs golden max "
+          f"{gerr.max():.4f} mean {gerr.mean():.4f} (emulator vs golden max {emeta['vs_golden_max']:.4f} mean "
+          f"{emeta['vs_golden_mean']:.4f}); mean |dlogprob| top20 {dlp:.4f}; argmax GPU {int(lg.argmax())} "
+          f"emulator {int(e.argmax())} golden {int(g.argmax())}", flush=True)
+    assert err.max() <= tol_max and err.mean() <= tol_mean
+    # against FP32: the argmax rule above and the reference gate's FAIL boundary (benchmark/gate.py:115)
+    assert int(lg.argmax()) in {int(g.argmax()), int(e.argmax())} and dlp <= 0.15
+    m.release_buffers()
+
+
 @pytest.mark.parametrize("name", ["1b", "1b-hd96", "2b"])
 def test_two_layer_full_size_vs_emulator(name):
     """The architectures truncated to two layers (one full-sequence layer, then the last-token layer) at
