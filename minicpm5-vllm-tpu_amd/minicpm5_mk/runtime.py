@@ -86,7 +86,15 @@ def expected_shapes(L: int, H: int, inter: int, n_q: int, n_kv: int, hd: int, qu
 
 
 class MkModel:
-    """A libmk model over device tensors in the reference layout (kept alive by this object)."""
+    """A libmk model over device tensors in the reference layout (kept alive by this object).
+
+    Each (bs, seq, logits) shape gets persistent device buffers (workspace, ids, outputs) that its
+    captured hipGraph is bound to; the buffers of the MAX_SHAPES most recently used shapes are kept (a
+    2B workspace at (32, 8192) is several GB).  An evicted shape allocates again on its next call; its
+    old graph, cached by libmk under the old buffer addresses, is only replayed if a call brings exactly
+    those addresses back, so it never touches memory that is not that call's."""
+
+    MAX_SHAPES = 8
 
     def __init__(self, weights: dict, embed: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
                  final_norm: torch.Tensor, quant: str, n_q: int, n_kv: int, head_dim: int, eps: float,
@@ -131,7 +139,7 @@ class MkModel:
                                   ctypes.c_void_p(self.packed.data_ptr()), nbytes.value, _stream(),
                                   ctypes.byref(handle)), "mk_model_create")
         self._h = handle
-        self._bufs = {}
+        self._bufs = collections.OrderedDict()
         self._lock = threading.Lock()
 
     @property
@@ -161,12 +169,15 @@ class MkModel:
         key = (bs, seq, want_logits)
         b = self._bufs.get(key)
         if b is None:
+            while len(self._bufs) >= self.MAX_SHAPES:   # least recently used shape out
+                self._bufs.popitem(last=False)
             dev, H, V = self.device, self.dims["H"], self.dims["V"]
             b = {"ws": torch.empty(self.workspace_bytes(bs, seq), dtype=torch.uint8, device=dev),
                  "ids": torch.empty(bs * seq, dtype=torch.int32, device=dev),
                  "hidden": torch.empty((max(8, bs), H), dtype=BF16, device=dev),
                  "logits": torch.empty((bs, V), dtype=F32, device=dev) if want_logits else None}
             self._bufs[key] = b
+        self._bufs.move_to_end(key)
         return b
 
     def release_buffers(self) -> None:
@@ -252,7 +263,7 @@ class MkModel:
         if getattr(self, "_h", None):
             load().mk_model_destroy(self._h)
             self._h = None
-        self._bufs = {}
+        self._bufs = collections.OrderedDict()
 
     def __del__(self):
         try:

@@ -722,6 +722,33 @@ def test_runtime_forward_repacks_after_in_place_update():
 
 
 @pytest.mark.gpu
+def test_per_shape_buffers_are_bounded():
+    """MkModel keeps the buffers of at most MAX_SHAPES shapes (least recently used out); a shape whose
+    buffers were dropped allocates new ones on its next call and returns the same bits as before."""
+    from minicpm5_mk.config import preset
+    from minicpm5_mk.engine import MkEngine
+    from minicpm5_mk.synth import random_token_ids
+
+    dev = _dev()
+    eng = MkEngine(preset("tiny"), quant="auto", max_model_len=2048, device=str(dev), log=lambda *a: None,
+                   precompile="")
+    m = eng.model
+    shapes = [(b, s) for s in (128, 256, 384, 512, 640) for b in (1, 2)]
+    assert len(shapes) > m.MAX_SHAPES
+    first = {}
+    for b, s in shapes:
+        ids = random_token_ids(b, s, seed=b * 1000 + s).reshape(-1).to(dev)
+        first[(b, s)] = m.forward(ids, b, s, logits=True)
+        assert len(m._bufs) <= m.MAX_SHAPES
+    assert (1, 128, True) not in m._bufs                 # the oldest shape was dropped
+    for b, s in shapes[:3]:                              # dropped shapes run again, bitwise as before
+        ids = random_token_ids(b, s, seed=b * 1000 + s).reshape(-1).to(dev)
+        h, lg = m.forward(ids, b, s, logits=True)
+        assert torch.equal(h, first[(b, s)][0]) and torch.equal(lg, first[(b, s)][1])
+    eng.close()
+
+
+@pytest.mark.gpu
 def test_precompile_captures_without_running():
     """MkModel.precompile (MINICPM5_MK_PRECOMPILE, model.py:690-698) captures one hipGraph per shape
     without running it: the output buffers keep their contents, the graph count grows by one per new
