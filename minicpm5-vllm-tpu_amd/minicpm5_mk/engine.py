@@ -16,7 +16,6 @@ and run through libmk (`MkModel`).
 """
 from __future__ import annotations
 
-import dataclasses
 import os
 import time
 from dataclasses import dataclass, field
@@ -199,4 +198,4 @@ class MkEngine:
 
 
 __all__ = ["MkEngine", "SamplingParams", "RequestOutput", "CompletionOutput", "NotEligible", "mk_seq_ok",
-           "eligible_batch", "dataclasses"]
+           "eligible_batch"]

@@ -30,8 +30,6 @@ FP32 golden, which is itself checked against transformers' Llama).
 """
 from __future__ import annotations
 
-import math
-
 import torch
 
 BF16 = torch.bfloat16

@@ -11,7 +11,6 @@ Pinned by invariants, not by restating the formulas:
 """
 import math
 
-import numpy as np
 import pytest
 import torch
 
