@@ -344,20 +344,28 @@ def test_full_model_vs_emulator(name, tol_max, tol_mean):
 # by make_emulator_fixture.py --quant ...) and vs the FP32 golden.  (quant, fixture tag, max, mean): bounds
 # 1.5x the measured GPU-vs-emulator error, as for the W8A8 fixtures above.  The emulations themselves err
 # vs FP32: fp8d max 0.628 / mean 0.117, mean |dlogprob| top-20 0.129, argmax the golden's #3 (token 6581,
-# 0.166 nats below the top-1: e4m3's 3-bit mantissa moves it); static int8 0.211 / 0.038, 0.050, top-1.
-# Argmax rule: the golden top-1 or the token the emulation of the same numerics picks.
-# Measured on MI355X: fp8d 0.329 / 0.058 (argmax = the emulation's), static int8 0.161 / 0.027.
-QVARIANTS = [("fp8d:qkv+gu|sq|lastbf16", "fp8d", 0.5, 0.087), ("int8:qkv+gu|sq|lastbf16", "int8", 0.25, 0.041)]
+# 0.166 nats below the top-1: e4m3's 3-bit mantissa moves it); static int8 0.211 / 0.038, 0.050, top-1; int8
+# with an int8 O and down projection 0.431 / 0.069, 0.071, top-1; 2B fp8d 1.393 / 0.231, 0.236 -- beyond the
+# reference gate's FAIL boundary (0.15) already in the emulation, its argmax the golden's rank 16.
+# Argmax rule: the golden top-1 or the token the emulation of the same numerics picks; not applied where
+# the emulation itself fails the gate (2B fp8d: the fp8 error, mean 0.23, is ~3x the golden's top-2 margin,
+# so the top token is noise on either side -- the GPU picked another one than the emulation).
+# Measured on MI355X (max / mean vs the emulation): 1B fp8d 0.329 / 0.058, static int8 0.161 / 0.027,
+# int8d with int8 O / down 0.352 / 0.062; 2B fp8d 0.727 / 0.136.
+QVARIANTS = [("1b", "fp8d:qkv+gu|sq|lastbf16", "fp8d", 0.5, 0.087),
+             ("1b", "int8:qkv+gu|sq|lastbf16", "int8", 0.25, 0.041),
+             ("1b", "int8d:qkv+gu+o+down|sq|lastbf16|fqkv|fmlp", "int8d", 0.53, 0.093),
+             ("2b", "fp8d:qkv+gu|sq|lastbf16", "fp8d", 1.09, 0.204)]
 
 
-@pytest.mark.parametrize("quant,tag,tol_max,tol_mean", QVARIANTS)
-def test_full_model_quant_variants(quant, tag, tol_max, tol_mean):
+@pytest.mark.parametrize("name,quant,tag,tol_max,tol_mean", QVARIANTS)
+def test_full_model_quant_variants(name, quant, tag, tol_max, tol_mean):
     from minicpm5_mk.synth import random_token_ids
 
-    fx = np.load(os.path.join(HERE, "golden", f"emulate_1b_{tag}_b1_s8192.npz"))
+    fx = np.load(os.path.join(HERE, "golden", f"emulate_{name}_{tag}_b1_s8192.npz"))
     emeta = json.loads(bytes(fx["meta"]).decode())
-    gold, meta = _golden("1b")
-    m = _full_model("1b", quant)
+    gold, meta = _golden(name)
+    m = _full_model(name, quant)
     assert emeta["quant"] == m.quant == quant
     ids = random_token_ids(1, 8192, seed=emeta["id_seed"])
     _, lg = m.forward(ids.reshape(-1).to(_dev()), 1, 8192, logits=True)
@@ -368,13 +376,18 @@ def test_full_model_quant_variants(quant, tag, tol_max, tol_mean):
     lp, lpg = torch.log_softmax(lg, -1), torch.log_softmax(g, -1)
     top = torch.topk(lpg, 20).indices
     dlp = float((lp[top] - lpg[top]).abs().mean())
-    print(f"[variant] {quant}: GPU vs emulator max {err.max():.4f} mean {err.mean():.4f}; vs golden max "
+    edlp = float((torch.log_softmax(e, -1)[top] - lpg[top]).abs().mean())
+    print(f"[variant] {name} {quant}: emulator mean |dlogprob| top20 {edlp:.4f}; GPU vs emulator max {err.max():.4f} mean {err.mean():.4f}; vs golden max "
           f"{gerr.max():.4f} mean {gerr.mean():.4f} (emulator vs golden max {emeta['vs_golden_max']:.4f} mean "
           f"{emeta['vs_golden_mean']:.4f}); mean |dlogprob| top20 {dlp:.4f}; argmax GPU {int(lg.argmax())} "
           f"emulator {int(e.argmax())} golden {int(g.argmax())}", flush=True)
     assert err.max() <= tol_max and err.mean() <= tol_mean
-    # against FP32: the argmax rule above and the reference gate's FAIL boundary (benchmark/gate.py:115)
-    assert int(lg.argmax()) in {int(g.argmax()), int(e.argmax())} and dlp <= 0.15
+    # against FP32: the reference gate's FAIL boundary (benchmark/gate.py:115) and the argmax rule above or,
+    # where the emulation of the same numerics is itself beyond that boundary, no more than 1.2x its error
+    if edlp <= 0.15:
+        assert int(lg.argmax()) in {int(g.argmax()), int(e.argmax())} and dlp <= 0.15
+    else:
+        assert dlp <= 1.2 * edlp
     m.release_buffers()
 
 
