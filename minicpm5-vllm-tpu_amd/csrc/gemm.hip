@@ -30,6 +30,14 @@ namespace {
 
 constexpr int BKB = 64;   // K bytes per LDS stage (two MFMA k-steps)
 
+// 32-column accumulator tiles per epilogue staging chunk: all NTL of them when the waves' 32-row slices
+// fit in the ring, else the most that do (whole epilogue passes of ew columns each).
+constexpr int epi_chunk(int ntl, int ew, int nw, int ring_bytes) {
+  int n = ntl;
+  while (n > 1 && ((n * 32) % ew != 0 || nw * 32 * (n * 128 + 16) > ring_bytes)) --n;
+  return n;
+}
+
 // Block tile BM x BN computed by WGM x WGN waves, NST-stage LDS ring.
 template <int BM_, int BN_, int WGM_, int WGN_, int NST_, int OCC_, int LOOP_ = 0>
 struct GemmCfg {
@@ -45,7 +53,10 @@ struct GemmCfg {
   // then B blocks; block b is loaded by wave b % NW.  Waves w < NL % NW load QH blocks, the rest QL.
   static constexpr int NA = BM / 16, NL = (BM + BN) / 16;
   static constexpr int QL = NL / NW, QH = (NL + NW - 1) / NW, NQH = NL % NW == 0 ? NW : NL % NW;
-  static constexpr int EROW = WN * 4 + 16;                // epilogue LDS row (f32 + pad)
+  static constexpr int EW = WN % 64 == 0 ? 64 : 32;       // epilogue pass width (columns)
+  static constexpr int ECH = epi_chunk(NTL, EW, NW, NST * ST_BYTES);   // 32-column tiles per staging chunk
+  static constexpr int NECH = (NTL + ECH - 1) / ECH;
+  static constexpr int EROW = ECH * 32 * 4 + 16;          // epilogue LDS row (f32 + pad)
   static_assert(BM % 16 == 0 && BN % 16 == 0 && NA % NW == 0, "load split: A blocks evenly over the waves");
   static_assert(LOOP == 1 || NL % NW == 0, "split k-step loop: the same load count on every wave");
   static_assert(NW * 32 * EROW <= NST * ST_BYTES, "epilogue staging fits in the ring");
@@ -55,6 +66,10 @@ struct GemmCfg {
   static_assert(LOOP != 2 || NST >= 5, "two-stage loop: stages it + 2, it + 3 land while it + 4 .. are in flight");
   static_assert(LOOP != 1 || (NW == 8 && NST >= 3 && NQH % 4 == 0),
                 "ping-pong needs two groups of four waves with uniform loads and two stages in flight");
+  // Lean addressing for ping-pong tiles whose accumulators and three operand sets nearly fill the 256
+  // registers of a wave: the async-load lane offsets that follow from others are recomputed where
+  // they are used instead of being held through the main loop (held, they spilled into the loop).
+  static constexpr bool LEAN = LOOP == 1 && 16 * MT * NTL + 12 * (MT + NTL) > 232;
 };
 // 256x256 block, 128x128 per wave (accumulators in AGPRs), one workgroup per CU
 using CfgL = GemmCfg<256, 256, 2, 2, 3, 1, 0>;
@@ -67,6 +82,9 @@ using CfgX = GemmCfg<256, 256, 2, 4, 4, 1, 1>;
 // 256x192 block, 8 waves of 64x96 (two per SIMD), one workgroup per CU: N = 1536 in 8 column tiles, so
 // M = 8192 fills exactly 256 CUs
 using CfgN = GemmCfg<256, 192, 4, 2, 4, 1, 1>;
+// 256x320 block, 8 waves of 64x160: N = 2560 (the QKV projection at hd 128) in 8 column tiles, one round
+// of 256 CUs at M = 8192 where 256x192 tiles take 1.75 rounds; its epilogue stages 128 + 32 columns
+using CfgW = GemmCfg<256, 320, 4, 2, 4, 1, 1>;
 // Short problems (few tiles, each K loop latency-bound): 8-stage rings, seven stages of loads in flight.
 // 128x128 block, 64x64 per wave; 64x128 block, 32x64 per wave; one workgroup per CU
 // (the 64x128 tile runs two stages per barrier: its waves have few MFMAs per stage to cover a barrier)
@@ -203,6 +221,22 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
       loff[j] = (uint32_t)min(n0 + r, g.N - 1) * (uint32_t)ldb + 16u * ((lane & 3) ^ swz(r));
     }
   }
+  // Lean addressing: load j's rows are 16 NW j rows past load 0's (A) or load JA's (B), with the same
+  // swizzle; the offset is clamped into the last row (rows past M / N are never stored).  The empty asm
+  // keeps the sum from being hoisted out of the loop into a register of its own.
+  const uint32_t lim_a = (uint32_t)(g.M - 1) * (uint32_t)lda + 48u, lim_b = (uint32_t)(g.N - 1) * (uint32_t)ldb + 48u;
+  auto voff = [&](int j) -> uint32_t {
+    if constexpr (!C::LEAN) {
+      return loff[j];
+    } else {
+      const bool isa = j < JA;
+      if (j == 0 || j == JA) return loff[j];
+      uint32_t o = isa ? loff[0] : loff[JA];
+      asm volatile("" : "+v"(o));
+      o += (uint32_t)((isa ? j : j - JA) * 16 * C::NW) * (uint32_t)(isa ? lda : ldb);
+      return min(o, isa ? lim_a : lim_b);
+    }
+  };
   // The operands as buffers for the async loads (buffer_load_dwordx4 ... lds): the lane's offset is loff,
   // the K offset goes in the instruction's scalar offset.  The buffer form is counted by vmcnt alone, so
   // the compiler waits for exactly the LDS operand reads an MFMA needs (with the FLAT-encoded global
@@ -213,8 +247,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
   // then B blocks)
   auto issue1 = [&](int j, int st, int kb) {
     char* dst = smem + st * C::ST_BYTES + (w + C::NW * j) * 1024;
-    if (j < JA) copy16_to_lds(rA, loff[j], (uint32_t)kb, dst);
-    else if (j < C::QL || qfull) copy16_to_lds(rB, loff[j], (uint32_t)kb, dst);
+    if (j < JA) copy16_to_lds(rA, voff(j), (uint32_t)kb, dst);
+    else if (j < C::QL || qfull) copy16_to_lds(rB, voff(j), (uint32_t)kb, dst);
   };
   // wait until at most `n` stages of this wave's async loads are outstanding
   auto wait_stages = [&](auto nc) {
@@ -266,7 +300,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
                       EPI == Epi::DQ_SILU_F32A || EPI == Epi::SILU_BF16;   // SILU_BF16: only with scales
   // the wave's columns are processed in passes of EW = 64 columns (32 when the width is not a multiple
   // of 64); a SiLU pass is one [32 gate | 32 up] block
-  constexpr int EW = C::WN % 64 == 0 ? 64 : 32;
+  constexpr int EW = C::EW;
   constexpr int NSB = C::WN / EW;
   constexpr int TPR = SILU ? EW / 16 : EW / 8;         // tasks per row
   constexpr int TRS = 64 / TPR;                        // rows between a lane's tasks
@@ -539,9 +573,10 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
   }
 
   // ---- epilogue through LDS.  The accumulators of a 32x32 tile sit column-wise across lanes (lane:
-  // column, 16 rows); each 32-row slice of the wave's tile is written to the wave's own LDS region,
-  // then every lane handles 8 consecutive columns of a row with 16-byte accesses.  The residual rows of
-  // slice mt + 1 are loaded while slice mt is processed.
+  // column, 16 rows); each 32-row slice of the wave's tile is written to the wave's own LDS region
+  // (in chunks of ECH 32-column tiles when the whole slice does not fit), then every lane handles 8
+  // consecutive columns of a row with 16-byte accesses.  The residual rows of slice mt + 1 are loaded
+  // while slice mt is processed.
   u32x4 rv[2][NSB][NTASK];
   auto load_res = [&](int mt, u32x4 (&dst)[NSB][NTASK]) {
 #pragma unroll
@@ -564,12 +599,19 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
       if (mt + 1 < C::MT) load_res(mt + 1, rv[(mt + 1) & 1]);
     }
 #pragma unroll
-    for (int nt = 0; nt < C::NTL; ++nt)
+    for (int ch = 0; ch < C::NECH; ++ch) {
+    // chunk ch: tiles [ch ECH, ch ECH + ECH) of the slice, wave columns [cb, ce), whole passes
+    constexpr int ECH = C::ECH;
+    const int cb = ch * ECH * 32, ce = min(C::WN, cb + ECH * 32);
+#pragma unroll
+    for (int nt = 0; nt < C::NTL; ++nt) {
+      if (nt < ch * ECH || nt >= (ch + 1) * ECH) continue;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int lr = 8 * (r >> 2) + 4 * half + (r & 3);
-        *reinterpret_cast<typename T::Elem*>(er + lr * EROW + (nt * 32 + col) * 4) = acc[mt][nt][r];
+        *reinterpret_cast<typename T::Elem*>(er + lr * EROW + ((nt - ch * ECH) * 32 + col) * 4) = acc[mt][nt][r];
       }
+    }
     __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's LDS writes are done
     __builtin_amdgcn_wave_barrier();
     const int mrow0 = m0 + wm * C::WM + mt * 32;
@@ -579,10 +621,11 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
       for (int sb = 0; sb < NSB; ++sb)
 #pragma unroll
       for (int i = 0; i < NTASK; ++i) {
+        if (sb * 64 < cb || sb * 64 >= ce) continue;
         const int p0 = nb0 + sb * 64, nh = p0 / 2 + j0;
         const int lr = trow0 + i * TRS, m = mrow0 + lr;
-        const V4* gp = reinterpret_cast<const V4*>(er + lr * EROW + (sb * 64 + j0) * 4);
-        const V4* up = reinterpret_cast<const V4*>(er + lr * EROW + (sb * 64 + 32 + j0) * 4);
+        const V4* gp = reinterpret_cast<const V4*>(er + lr * EROW + (sb * 64 - cb + j0) * 4);
+        const V4* up = reinterpret_cast<const V4*>(er + lr * EROW + (sb * 64 - cb + 32 + j0) * 4);
         const V4 g0 = gp[0], g1 = gp[1], u0 = up[0], u1 = up[1];
         if (m >= g.M || p0 >= g.N) continue;
         float h[8];
@@ -621,6 +664,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
     } else {
 #pragma unroll
       for (int sb = 0; sb < NSB; ++sb) {
+      if (sb * EW < cb || sb * EW >= ce) continue;
       if constexpr (ROUTE) {
         // QKV routing (q, K and V blocks start at multiples of 64 columns, so a pass is all one of them).
         // V columns: lane task =
@@ -646,7 +690,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
 #pragma unroll
             for (int i = 0; i < NTASK; ++i) {
               const int lr = trow0 + i * TRS;
-              const V4* vp = reinterpret_cast<const V4*>(er + lr * EROW + (sb * EW + tcol * 8) * 4);
+              const V4* vp = reinterpret_cast<const V4*>(er + lr * EROW + (sb * EW - cb + tcol * 8) * 4);
               const V4 q0 = vp[0], q1 = vp[1];
               float v[8];
 #pragma unroll
@@ -690,7 +734,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
 #pragma unroll
               for (int e = 0; e < 8; ++e)
                 v[e] = T::f(*reinterpret_cast<const typename T::Elem*>(er + ((e < 4 ? ra : rb) + (e & 3)) * EROW +
-                                                                       (sb * EW + cc) * 4));
+                                                                       (sb * EW - cb + cc) * 4));
               if constexpr (DQ) {
                 const f32x4 sa = *reinterpret_cast<const f32x4*>(g.rs + mrow0 + ra);
                 const f32x4 sb4 = *reinterpret_cast<const f32x4*>(g.rs + mrow0 + rb);
@@ -714,7 +758,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
       for (int i = 0; i < NTASK; ++i) {
         const int c8 = sb * EW + tcol * 8, n = nb0 + c8;
         const int lr = trow0 + i * TRS, m = mrow0 + lr;
-        const V4* vp = reinterpret_cast<const V4*>(er + lr * EROW + c8 * 4);
+        const V4* vp = reinterpret_cast<const V4*>(er + lr * EROW + (c8 - cb) * 4);
         const V4 r0 = vp[0], r1 = vp[1];
         if (m >= g.M || n >= g.N) continue;
         if constexpr (EPI == Epi::I32) {
@@ -766,6 +810,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
       }
     }
     __builtin_amdgcn_wave_barrier();
+    }
   }
 }
 
@@ -911,15 +956,19 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(GemmArgs g, int spli
 // them evenly), so the estimate is ceil(tiles / 256) * tile area / relative throughput, the throughputs
 // measured on MI355X at the model's shapes (random data): the 8-wave ping-pong 256x256 tile is fastest
 // per tile, except for the SiLU epilogue, whose VALU work is hidden better by two co-resident
-// 256x128 workgroups.
+// 256x128 workgroups.  The 256x320 tile's 1.14: the QKV shape M = 8192, N = 2560, K = 1536 (dequantising
+// epilogue, no routing) takes 40.9 us on it, 48.6 us on 256x192 tiles (1.75 rounds) and 52.3 us on
+// 256x256 ones (1.25 rounds).
 int choose_cfg(const GemmArgs& g) {
   const bool silu = g.epi == Epi::DQ_SILU || g.epi == Epi::DQ_SILU_F32A || g.epi == Epi::SILU_BF16;
-  if (g.cfg >= 1 && g.cfg <= 7 && !(silu && g.cfg == 5)) return g.cfg;
+  // 5 and 8 (96- and 160-column waves) cannot hold whole [gate | up] blocks
+  auto ok = [&](int id) { return id >= 1 && id <= 8 && !(silu && (id == 5 || id == 8)); };
+  if (ok(g.cfg)) return g.cfg;
   static const int forced = [] {
-    const char* e = std::getenv("MK_GEMM_CFG");   // tuning override: 1 .. 7
+    const char* e = std::getenv("MK_GEMM_CFG");   // tuning override: 1 .. 8
     return e ? std::atoi(e) : 0;
   }();
-  if (forced >= 1 && forced <= 7 && !(silu && forced == 5)) return forced;
+  if (ok(forced)) return forced;
   // Few tiles (short prompts, e.g. M <= 1024): each tile's K loop is latency-bound, so the 64x128 tile
   // whose loop runs two stages per barrier wins whenever its tiling fits one round of 256 CUs (measured
   // on MI355X at M = 128 - 1024: the 1B gate/up at M = 128 takes 7.6 us on it, 14.0 on 256x128; the 1B
@@ -932,12 +981,12 @@ int choose_cfg(const GemmArgs& g) {
     if (nk >= 64 && tiles(128, 128) <= 256) return 6;
   }
   struct Opt { int id, bm, bn; double eff; };
-  const Opt opts[5] = {{4, 256, 256, silu ? 1.05 : 1.25}, {2, 256, 128, 1.0}, {1, 256, 256, 0.9},
-                       {3, 128, 128, 0.85}, {5, 256, 192, 1.15}};
+  const Opt opts[6] = {{4, 256, 256, silu ? 1.05 : 1.25}, {2, 256, 128, 1.0}, {1, 256, 256, 0.9},
+                       {3, 128, 128, 0.85}, {5, 256, 192, 1.15}, {8, 256, 320, 1.14}};
   int best = 2;
   double bt = 1e300;
   for (const Opt& o : opts) {
-    if (silu && (o.id == 3 || o.id == 5)) continue;   // 3: never faster; 5: 96-column waves (no SiLU)
+    if (silu && (o.id == 3 || o.id == 5 || o.id == 8)) continue;   // 3: never faster; 5, 8: no SiLU
     const double tiles = (double)((g.M + o.bm - 1) / o.bm) * ((g.N + o.bn - 1) / o.bn);
     const double t = std::ceil(tiles / 256.0) * o.bm * o.bn / o.eff;
     if (t < bt * 0.999) {
@@ -996,6 +1045,10 @@ void launch_t(const GemmArgs& g, hipStream_t st) {
     case 4: launch_c<CfgX, IN, EPI>(g, st); break;
     case 5:   // 96-column waves cannot hold whole [gate | up] blocks: SiLU epilogues take the 256x128 tile
       if constexpr (!silu) launch_c<CfgN, IN, EPI>(g, st);
+      else launch_c<CfgM, IN, EPI>(g, st);
+      break;
+    case 8:   // 160-column waves: likewise
+      if constexpr (!silu) launch_c<CfgW, IN, EPI>(g, st);
       else launch_c<CfgM, IN, EPI>(g, st);
       break;
     case 6: launch_c<CfgD, IN, EPI>(g, st); break;

@@ -82,7 +82,8 @@ struct GemmArgs {
   const float* aux;           // DQ_SILU_F32A: per-intermediate-channel factor
   int cfg;                    // tile configuration: 0 auto, 1 256x256 (4 waves), 2 256x128, 3 128x128,
                               // 4 256x256 (8 waves), 5 256x192 (8 waves; not for the SiLU epilogues),
-                              // 6 128x128 and 7 64x128 with 8-stage rings (short, long-K problems)
+                              // 6 128x128 and 7 64x128 with 8-stage rings (short, long-K problems),
+                              // 8 256x320 (8 waves; not for the SiLU epilogues)
   int gm;                     // tile-order group height (rows of tiles); 0 = chosen by the launcher
   void* ws;                   // skinny GEMM: optional f32 workspace for split-K partials (null = no split)
   size_t ws_bytes;

@@ -187,9 +187,11 @@ def test_row_quant_scale_tree_bitexact(T, H):
     assert np.array_equal(sx.cpu().numpy().view(np.uint32), ref.view(np.uint32))
 
 
-@pytest.mark.parametrize("M,N,K", [(256, 128, 64), (300, 200, 1536), (8192, 1920, 1536), (1000, 1536, 4608),
-                                   (1000, 1536, 1088)])
+@pytest.mark.parametrize("M,N,K", [(256, 128, 64), (300, 200, 1536), (8192, 1920, 1536), (8192, 2560, 1536),
+                                   (1000, 1536, 4608), (1000, 1536, 1088)])
 def test_gemm_int8_exact(M, N, K):
+    """Exact int32 products; (8192, 1920) and (8192, 2560) (the QKV projections at hd 96 and 128) take the
+    256x320 tile, whose epilogue stages its 64x160 wave tiles in two column chunks."""
     from minicpm5_mk import ops
     from oracle import emulate
 
@@ -263,6 +265,35 @@ def test_gemm_bf16_rows_independent_of_tile(N, K):
     big = ops.gemm(a, b, "f32")
     small = ops.gemm(a[:1000].contiguous(), b, "f32")
     assert torch.equal(small.view(torch.int32), big[:1000].view(torch.int32))
+
+
+@pytest.mark.parametrize("epi", ["f32", "bf16", "res_f32add", "res_bf16add"])
+def test_gemm_wide_tile_rows_match(epi):
+    """M = 8192, N = 2560 takes the 256x320 tile (one round of 256 CUs; 64x160 wave tiles, the epilogue
+    staged in a 128- and a 32-column chunk, the offsets of later async loads recomputed per load), M = 1000
+    the 256x192 one: the first 1000 rows are bitwise equal for each epilogue, and the f32 products match
+    a float64 reference on rows at both ends."""
+    from minicpm5_mk import ops
+
+    dev = _dev()
+    g = torch.Generator().manual_seed(2560)
+    M, N, K = 8192, 2560, 1536
+    a = torch.randn(M, K, generator=g).to(BF16)
+    b = (torch.randn(N, K, generator=g) * 0.02).to(BF16)
+    x = torch.randn(M, N, generator=g).to(BF16)
+    ad, bd = a.to(dev), b.to(dev)
+    if epi.startswith("res"):
+        big = ops.gemm(ad, bd, epi, res=x.clone().to(dev))
+        small = ops.gemm(ad[:1000].contiguous(), bd, epi, res=x[:1000].clone().to(dev))
+    else:
+        big = ops.gemm(ad, bd, epi)
+        small = ops.gemm(ad[:1000].contiguous(), bd, epi)
+    assert torch.equal(small.view(torch.int16 if small.dtype == BF16 else torch.int32),
+                       big[:1000].view(torch.int16 if big.dtype == BF16 else torch.int32))
+    if epi == "f32":
+        rows = torch.cat([torch.arange(300), torch.arange(M - 300, M)])
+        ref = a[rows].double() @ b.double().t()
+        torch.testing.assert_close(big.cpu()[rows].double(), ref, rtol=1e-4, atol=1e-4 * ref.abs().max().item())
 
 
 def test_gemm_residual_epilogues():
