@@ -296,6 +296,58 @@ def test_gemm_wide_tile_rows_match(epi):
         torch.testing.assert_close(big.cpu()[rows].double(), ref, rtol=1e-4, atol=1e-4 * ref.abs().max().item())
 
 
+_RAGGED_WIDE = r"""
+import sys, torch
+sys.path[:0] = [sys.argv[1], sys.argv[2]]
+from minicpm5_mk import ops
+from oracle import emulate
+dev = torch.device("cuda:0")
+g = torch.Generator().manual_seed(77)
+bad = []
+for M, N, K in [(300, 200, 1536), (1000, 600, 64), (257, 328, 128), (8292, 2568, 1536)]:
+    a = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
+    b = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    print(f"[wide ragged] int8 {M}x{N}x{K}", flush=True)
+    acc = ops.gemm(a.to(dev), b.to(dev), "i32").cpu().to(torch.int64)
+    if not torch.equal(acc, emulate.int_matmul(a, b.t().contiguous())):
+        bad.append(("i32", M, N, K))
+for M, N, K, epi in [(300, 200, 1536, "f32"), (1000, 600, 2048, "f32"), (333, 640, 512, "res_f32add")]:
+    a = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    b = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    x = torch.randn(M, N, generator=g).to(torch.bfloat16)
+    print(f"[wide ragged] bf16 {epi} {M}x{N}x{K}", flush=True)
+    ref = a.double() @ b.double().t()
+    if epi == "f32":
+        out = ops.gemm(a.to(dev), b.to(dev), "f32").cpu().double()
+        ok = ((out - ref).abs() <= 1e-4 * ref.abs().max()).all()
+    else:
+        out = ops.gemm(a.to(dev), b.to(dev), epi, res=x.clone().to(dev)).cpu().float()
+        exp = (x.float() + ref.float())
+        ok = ((out - exp).abs() <= exp.abs() * 2.0 ** -7 + 1e-3).all()
+    if not bool(ok):
+        bad.append((epi, M, N, K))
+print("BAD", bad, flush=True)
+sys.exit(1 if bad else 0)
+"""
+
+
+def test_gemm_wide_tile_ragged_shapes():
+    """The 256x320 tile forced for every GEMM (MK_GEMM_CFG=8, a fresh process: the override is read once)
+    on shapes that are not tile multiples -- rows past M and columns past N take the clamped load offsets
+    of the lean addressing and the bounds checks of the chunked epilogue: exact int32 products against the
+    oracle, bf16 products and the f32 residual epilogue against float64."""
+    import os
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, MK_GEMM_CFG="8")
+    r = subprocess.run([sys.executable, "-c", _RAGGED_WIDE, root, os.path.join(root, "minicpm5-vllm-tpu_amd")],
+                       env=env, capture_output=True, text=True, timeout=240)
+    print(r.stdout[-2000:], r.stderr[-2000:])
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
+
+
 def test_gemm_residual_epilogues():
     from minicpm5_mk import ops
 
