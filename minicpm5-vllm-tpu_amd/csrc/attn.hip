@@ -451,10 +451,11 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_fwd_kernel(
       for (int r = 0; r < 16; ++r) scur[c][r] -= m;   // scores are kept relative to m from here on
 
     // ---- steady state: step t computes QK(t+1), softmax + PV(t) and stages K(t+3), V(t+2) into the
-    // slots K(t-1), V(t-2) left.  A workgroup barrier follows every odd step; between two barriers a wave
-    // is at most one step ahead of another, and the 4-slot rings keep the tiles that either step
-    // reads apart from the ones that either step writes.  The waves of a SIMD run together, so a wave
-    // overlaps its own VALU work with its MFMAs, spread evenly over the step: the QK(t+1) MFMAs carry
+    // slots K(t-1), V(t-2) left.  A workgroup barrier follows every even step (step 0's also orders the
+    // QK(0) before the loop ahead of step 1's refill of its K slot); between two barriers a wave is at
+    // most one step ahead of another, and the 4-slot rings keep the tiles that either step reads apart
+    // from the ones that either step writes.  The waves of a SIMD run together,
+    // so a wave overlaps its own VALU work with its MFMAs, spread evenly over the step: the QK(t+1) MFMAs carry
     // the softmax of keys 0..31 of tile t (exp2, bf16 P, row sum), the first half of the PV(t) MFMAs
     // (which use those keys) the softmax of keys 32..63, the second half the row max of tile t+1.  Each
     // MFMA is issued with a slice of the VALU work; LDS operands are read PF MFMAs ahead.  Only the last
@@ -465,8 +466,10 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_fwd_kernel(
     static_assert(NPC < NPV && softmax_deadlines_ok(NQC, DT), "softmax chunks must be ready for their PV MFMAs");
     auto step = [&](auto mask, int t, const f32x16 (&sc)[2], f32x16 (&sn)[2]) {
       constexpr bool MASK = decltype(mask)::value;
-      // K(t+3), V(t+2) into the slots K(t-1), V(t-2) left (last read in step t-2); clamped reloads at
-      // the end land in free slots.  The copies are awaited before the next barrier.
+      // K(t+3), V(t+2) into the slots K(t-1), V(t-2) left, last read in step t-2 (K(0)'s, refilled in
+      // step 1, in the QK(0) before step 0): one of steps t-2, t-1 is even, so that read is behind a
+      // barrier.  Clamped reloads at the end land in free slots.  The copies are awaited before the next
+      // barrier.
       aload_k(min(t + 3, nkt - 1), (t + 3) % L::NK);
       aload_v(min(t + 2, nkt - 1), (t + 2) % L::NV);
       const char* ksl = kring + ((t + 1) % L::NK) * L::KBYTES;
@@ -555,7 +558,7 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_fwd_kernel(
 #pragma unroll
           for (int r = 0; r < 16; ++r) sn[c][r] -= d;
       }
-      if (t & 1) {
+      if (!(t & 1)) {
         __builtin_amdgcn_s_waitcnt(0);   // this wave's copies of steps t-1 and t have landed
         __syncthreads();
       }
