@@ -172,10 +172,13 @@ class MkModel:
             while len(self._bufs) >= self.MAX_SHAPES:   # least recently used shape out
                 self._bufs.popitem(last=False)
             dev, H, V = self.device, self.dims["H"], self.dims["V"]
-            b = {"ws": torch.empty(self.workspace_bytes(bs, seq), dtype=torch.uint8, device=dev),
-                 "ids": torch.empty(bs * seq, dtype=torch.int32, device=dev),
-                 "hidden": torch.empty((max(8, bs), H), dtype=BF16, device=dev),
-                 "logits": torch.empty((bs, V), dtype=F32, device=dev) if want_logits else None}
+            # ordinary tensors even when the first call of a shape runs under torch.inference_mode (vLLM's
+            # model runner): `ids` is written in place on every call, also outside inference mode
+            with torch.inference_mode(False):
+                b = {"ws": torch.empty(self.workspace_bytes(bs, seq), dtype=torch.uint8, device=dev),
+                     "ids": torch.empty(bs * seq, dtype=torch.int32, device=dev),
+                     "hidden": torch.empty((max(8, bs), H), dtype=BF16, device=dev),
+                     "logits": torch.empty((bs, V), dtype=F32, device=dev) if want_logits else None}
             self._bufs[key] = b
         self._bufs.move_to_end(key)
         return b
@@ -275,9 +278,16 @@ class MkModel:
 # runtime.forward's packed models: key (storage, shapes, quant, shape arguments) -> (version counters of
 # the tensors, MkModel), least recently used first.  The packed copy is rebuilt when a caller updated
 # any of the tensors in place (torch bumps a tensor's version counter on every in-place write), as the
-# reference op reads the tensors it is passed on every call.
+# reference op reads the tensors it is passed on every call.  The MkModel holds the tensors, so their
+# storage cannot be freed and reused under the same key while cached.
 _MODELS: "collections.OrderedDict" = collections.OrderedDict()
 MAX_CACHED_MODELS = 2
+
+
+def _version(t: torch.Tensor) -> int:
+    """The tensor's version counter; inference tensors (made under torch.inference_mode, as vLLM's model
+    runner runs) keep none, so an in-place update of one is not seen: -1."""
+    return -1 if t.is_inference() else t._version
 
 
 def _validate_attn(attn: str) -> None:
@@ -297,7 +307,7 @@ def forward(input_ids, embed, cos, sin, final_norm, w_qkv, w_o, w_gu, w_down, s_
                a_qkv, a_o, a_gu, a_down, wl_qkv, wl_o, wl_gu, wl_down)
     key = (tuple(t.data_ptr() for t in tensors), tuple(tuple(t.shape) for t in tensors), quant, n_q, n_kv,
            head_dim, float(eps))
-    versions = tuple(t._version for t in tensors)
+    versions = tuple(_version(t) for t in tensors)
     hit = _MODELS.get(key)
     if hit is not None and hit[0] != versions:        # updated in place since it was packed: re-pack
         _MODELS.pop(key)[1].close()

@@ -736,6 +736,41 @@ def test_runtime_forward_repacks_after_in_place_update():
 
 
 @pytest.mark.gpu
+def test_runtime_forward_inference_tensors():
+    """vLLM's model runner works under torch.inference_mode, so the op may get inference tensors, which
+    have no version counter: runtime.forward takes them, called in inference mode and then outside it
+    (the per-shape buffers made in inference mode stay writable), and returns the bits it returns for
+    ordinary tensors."""
+    from minicpm5_mk import runtime
+    from minicpm5_mk.config import preset
+    from minicpm5_mk.mk_weights import prepare_mk_weights
+    from minicpm5_mk.runtime import WEIGHT_ORDER
+    from minicpm5_mk.synth import random_hf_state_dict, random_token_ids
+
+    dev = _dev()
+    cfg = preset("tiny")
+    quant = "int8d:qkv+gu|sq|lastbf16|fqkv|fmlp"
+    sd = random_hf_state_dict(cfg)
+    w = prepare_mk_weights(sd, cfg.as_mk_cfg(), quant, 1024, log=lambda *a: None)
+    bs, seq = 1, 384
+    args = (bs, seq, quant, cfg.n_q, cfg.n_kv, cfg.head_dim, cfg.eps, "auto")
+    ids = random_token_ids(bs, seq, seed=5).reshape(-1).to(dev)
+    host = [sd["model.embed_tokens.weight"], w["cos"], w["sin"], sd["model.norm.weight"]] + [w[k] for k in WEIGHT_ORDER]
+    runtime.clear_cache()
+    ref = runtime.forward(ids, *[t.to(dev) for t in host], *args)
+    runtime.clear_cache()
+    with torch.inference_mode():
+        inf = [t.to(dev) for t in host]
+        assert all(t.is_inference() for t in inf)
+        out = runtime.forward(ids, *inf, *args)
+        again = runtime.forward(ids, *inf, *args)
+    outside = runtime.forward(ids, *inf, *args)
+    assert len(runtime._MODELS) == 1
+    assert torch.equal(out, ref) and torch.equal(again, ref) and torch.equal(outside, ref)
+    runtime.clear_cache()
+
+
+@pytest.mark.gpu
 def test_per_shape_buffers_are_bounded():
     """MkModel keeps the buffers of at most MAX_SHAPES shapes (least recently used out); a shape whose
     buffers were dropped allocates new ones on its next call and returns the same bits as before."""
