@@ -222,8 +222,10 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_kernel(GemmArgs g) {
     }
   }
   // Lean addressing: load j's rows are 16 NW j rows past load 0's (A) or load JA's (B), with the same
-  // swizzle; the offset is clamped into the last row (rows past M / N are never stored).  The empty asm
-  // keeps the sum from being hoisted out of the loop into a register of its own.
+  // swizzle; the offset is clamped into the last row (rows past M / N are never stored), whose last
+  // 16-byte chunk plus the largest K offset still ends inside the buffer (the range check covers the
+  // lane offset only).  The empty asm keeps the sum from being hoisted out of the loop into a register
+  // of its own.
   const uint32_t lim_a = (uint32_t)(g.M - 1) * (uint32_t)lda + 48u, lim_b = (uint32_t)(g.N - 1) * (uint32_t)ldb + 48u;
   auto voff = [&](int j) -> uint32_t {
     if constexpr (!C::LEAN) {
