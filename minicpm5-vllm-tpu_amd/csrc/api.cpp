@@ -30,19 +30,23 @@ namespace {
 template <class F>
 int time_launches(F launch, int iters, hipStream_t st, float* avg_ms) {
   MK_REQUIRE(iters >= 1 && avg_ms != nullptr, "bench: iters must be >= 1 and avg_ms non-null");
-  hipEvent_t e0, e1;
-  MK_HIP_CHECK(hipEventCreate(&e0));
-  MK_HIP_CHECK(hipEventCreate(&e1));
+  struct Events {   // destroyed on every return path
+    hipEvent_t e[2] = {nullptr, nullptr};
+    ~Events() {
+      for (hipEvent_t x : e)
+        if (x) hipEventDestroy(x);
+    }
+  } ev;
+  MK_HIP_CHECK(hipEventCreate(&ev.e[0]));
+  MK_HIP_CHECK(hipEventCreate(&ev.e[1]));
   int rc = launch();   // untimed first launch: code-object load and cold caches stay out of the average
   MK_HIP_CHECK(hipStreamSynchronize(st));
-  MK_HIP_CHECK(hipEventRecord(e0, st));
+  MK_HIP_CHECK(hipEventRecord(ev.e[0], st));
   for (int i = 0; i < iters && rc == MK_OK; ++i) rc = launch();
-  MK_HIP_CHECK(hipEventRecord(e1, st));
-  MK_HIP_CHECK(hipEventSynchronize(e1));
+  MK_HIP_CHECK(hipEventRecord(ev.e[1], st));
+  MK_HIP_CHECK(hipEventSynchronize(ev.e[1]));
   float ms = 0.f;
-  MK_HIP_CHECK(hipEventElapsedTime(&ms, e0, e1));
-  hipEventDestroy(e0);
-  hipEventDestroy(e1);
+  MK_HIP_CHECK(hipEventElapsedTime(&ms, ev.e[0], ev.e[1]));
   if (rc) return rc;
   *avg_ms = ms / iters;
   return MK_OK;
