@@ -291,8 +291,9 @@ def _cpu_model():
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    # the reference harness's method: 5 untimed + 50 timed forwards per shape (run_benchmark.py:39, 92-93)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--arch", default="1b", help="1b (hd 128, reference HF config) | 1b-hd96 | 2b")
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--seq", type=int, default=8192)
