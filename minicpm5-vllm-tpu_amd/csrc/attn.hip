@@ -449,6 +449,19 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_fwd_kernel(
     for (int c = 0; c < 2; ++c)
 #pragma unroll
       for (int r = 0; r < 16; ++r) scur[c][r] -= m;   // scores are kept relative to m from here on
+    // -m in all 16 accumulator slots, kept in registers and rebuilt only when m changes: the C operand of
+    // every step's first two QK MFMAs, so the scores come out of the matrix core as S - m with no
+    // subtraction per score and no per-step accumulator set-up.  Built as 8 register pairs.
+    f32x16 nmb;
+    auto set_nmb = [&]() {
+      u64x8 nm;
+      const uint64_t bb = __float_as_uint(-m);
+      nm[0] = (bb << 32) | bb;
+#pragma unroll
+      for (int i = 1; i < 8; ++i) nm[i] = mov64(nm[0]);
+      nmb = __builtin_bit_cast(f32x16, nm);
+    };
+    set_nmb();
 
     // ---- steady state: step t computes QK(t+1), softmax + PV(t) and stages K(t+3), V(t+2) into the
     // slots K(t-1), V(t-2) left.  A workgroup barrier follows every even step (step 0's also orders the
@@ -489,17 +502,8 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_fwd_kernel(
         psum = dot2_bf16_sum(pb[c][s2][e], psum);
       };
       float mx = -INFINITY;
-      {
-        // the QK MFMAs accumulate onto -m: S - m with no subtraction per score.  -m is built in all 16
-        // accumulator slots as 8 register pairs (9 instructions, not 16)
-        u64x8 nm;
-        const uint64_t b = __float_as_uint(-m);
-        nm[0] = (b << 32) | b;
-#pragma unroll
-        for (int i = 1; i < 8; ++i) nm[i] = mov64(nm[0]);
-        sn[0] = __builtin_bit_cast(f32x16, nm);
-        sn[1] = sn[0];
-      }
+      sn[0] = nmb;   // the QK MFMAs accumulate onto -m
+      sn[1] = nmb;
 #pragma unroll
       for (int j = 0; j < PF; ++j) kr[j] = kread(j);
 #pragma unroll
@@ -553,6 +557,8 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_fwd_kernel(
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
         m += d;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) nmb[r] -= d;   // -m - d == -(m + d) exactly
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
