@@ -139,8 +139,6 @@ int launch_embed(const int32_t* ids, const uint16_t* embed, uint16_t* x, int T, 
 int launch_gather_last(const uint16_t* x, uint16_t* rows, int B, int S, int H, hipStream_t st);
 // h = bf16(bf16(silu(g)) * u) over (B, I) with gu (B, 2, I) bf16 (last layer)
 int launch_silu_mul_bf16(const uint16_t* gu, uint16_t* h, int B, int I, hipStream_t st);
-// x = bf16(x + y) (bf16 residual add)
-int launch_add_bf16(uint16_t* x, const uint16_t* y, size_t n, hipStream_t st);
 // zero fill (graph-safe replacement for memset)
 int launch_zero(void* p, size_t bytes, hipStream_t st);
 

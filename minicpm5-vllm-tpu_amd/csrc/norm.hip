@@ -236,11 +236,6 @@ __global__ void silu_mul_bf16_kernel(const uint16_t* __restrict__ gu, uint16_t* 
   }
 }
 
-__global__ void add_bf16_kernel(uint16_t* __restrict__ x, const uint16_t* __restrict__ y, size_t n) {
-  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
-    x[i] = f2bf(bf2f(x[i]) + bf2f(y[i]));
-}
-
 __global__ void zero_kernel(uint32_t* __restrict__ p, size_t nwords) {
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < nwords; i += (size_t)gridDim.x * blockDim.x)
     p[i] = 0u;
@@ -328,13 +323,6 @@ int launch_silu_mul_bf16(const uint16_t* gu, uint16_t* h, int B, int I, hipStrea
   const size_t n = (size_t)B * I;
   const int blocks = (int)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
   hipLaunchKernelGGL(silu_mul_bf16_kernel, dim3(blocks), dim3(256), 0, st, gu, h, B, I);
-  MK_HIP_CHECK(hipGetLastError());
-  return MK_OK;
-}
-
-int launch_add_bf16(uint16_t* x, const uint16_t* y, size_t n, hipStream_t st) {
-  const int blocks = (int)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
-  hipLaunchKernelGGL(add_bf16_kernel, dim3(blocks), dim3(256), 0, st, x, y, n);
   MK_HIP_CHECK(hipGetLastError());
   return MK_OK;
 }
