@@ -61,9 +61,11 @@ def ring_errors(nkt: int, barrier_parity: int):
 
 
 def test_ring_schedule_race_free():
-    """Every key-tile count a q tile can have at S <= 16384 (nkt = 1 .. 256): no read misses its tile and no
-    slot is refilled under a read."""
-    for nkt in range(1, 257):
+    """Every key-tile count a q tile can have at S <= 16384 (nkt = 1 .. 256), and samples up to S = 65536:
+    no read misses its tile and no slot is refilled under a read.  The steady schedule repeats every two
+    steps (four ring slots, one barrier), so the prologue, the tail cases of both step parities and a
+    few periods cover every length."""
+    for nkt in list(range(1, 257)) + [300, 511, 512, 513, 1023, 1024]:
         assert ring_errors(nkt, barrier_parity=0) == [], nkt
 
 
